@@ -1,0 +1,1208 @@
+// C-ABI runtime of the gfx950 quantized-weight inference path.
+//
+// Host side of the drop-in boundary declared in include/srq.h: executor
+// (kernelExecutor), weight handles (Param), model storage and loading
+// (loadHFModelFormatKV + readParam), paged KV pools (pagePool/KVCache), the
+// batched step (prefillSelected) and greedy generation (inferHFIDs), all of
+// cmd/monolith/monolith.go.  Every GPU computation is a HIP kernel of this
+// library; there is no CPU fallback.
+#include <algorithm>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "srq_internal.h"
+
+namespace srq {
+
+static thread_local std::string g_err;
+
+int fail(int code, const char *fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+
+void clear_error() { g_err.clear(); }
+
+namespace {
+
+std::mutex g_prep_mu;
+std::vector<char> g_prepared;
+
+int prepare_device(int device) {
+    std::lock_guard<std::mutex> lock(g_prep_mu);
+    if ((int)g_prepared.size() <= device) g_prepared.resize(device + 1, 0);
+    if (g_prepared[device]) return SRQ_OK;
+    SRQ_CHECK(gemv_prepare());
+    SRQ_CHECK(attention_prepare());
+    g_prepared[device] = 1;
+    return SRQ_OK;
+}
+
+struct DevBuf {
+    void *p = nullptr;
+    size_t n = 0;
+};
+
+int ensure(DevBuf &b, size_t bytes, hipStream_t s) {
+    if (bytes <= b.n) return SRQ_OK;
+    if (b.p) {
+        SRQ_HIP(hipStreamSynchronize(s));
+        SRQ_HIP(hipFree(b.p));
+        b.p = nullptr;
+        b.n = 0;
+    }
+    size_t want = std::max(bytes, (size_t)256);
+    if (hipMalloc(&b.p, want) != hipSuccess) {
+        b.p = nullptr;
+        return fail(SRQ_ENOMEM, "device allocation of %zu bytes failed", want);
+    }
+    b.n = want;
+    return SRQ_OK;
+}
+
+void release(DevBuf &b) {
+    if (b.p) (void)hipFree(b.p);
+    b.p = nullptr;
+    b.n = 0;
+}
+
+template <class T>
+T *as(DevBuf &b) {
+    return (T *)b.p;
+}
+
+int matrix_format(const std::string &format, bool embed_or_head) {
+    if (format == "f32") return SRQ_F32;
+    if (format == "q8") return SRQ_Q8;
+    if (format == "q4") return SRQ_Q4;
+    return embed_or_head ? SRQ_Q8 : SRQ_Q4;  // q4-mixed (M:572-582)
+}
+
+// hfInverseFrequency (M:4961-4977) with Transformers' f32 steps.
+float inverse_frequency(const srq_model_config &c, int head_dim, int index) {
+    float e = (float)(2 * index) / (float)head_dim;
+    float inv = 1.0f / (float)std::pow(c.rope_theta, (double)e);
+    if (!c.rope_llama3) return inv;
+    volatile float two_pi = (float)(2 * M_PI);
+    float wave = two_pi / inv;
+    float low_wave = (float)((double)c.rope_original / c.rope_low);
+    float high_wave = (float)((double)c.rope_original / c.rope_high);
+    float factor = (float)c.rope_factor;
+    if (wave > low_wave) return inv / factor;
+    if (wave >= high_wave) {
+        volatile float t = (float)c.rope_original / wave;
+        float smooth = (t - (float)c.rope_low) / (float)(c.rope_high - c.rope_low);
+        volatile float a = (1 - smooth) * inv;
+        volatile float b = a / factor;
+        volatile float d = smooth * inv;
+        return b + d;
+    }
+    return inv;
+}
+
+}  // namespace
+}  // namespace srq
+
+using namespace srq;
+
+// ------------------------------------------------------------------ handles
+// Activation workspace of one executor or decoder (decodeWorkspace,
+// M:6062-6100).  Captured graphs point into a decoder's own workspace, so a
+// later step that grows the executor's workspace cannot invalidate them.
+struct Workspace {
+    DevBuf X, N, Q, A, T, H, W2, LOG, LOGC, meta, flags;
+    void release_all() {
+        for (DevBuf *b : {&X, &N, &Q, &A, &T, &H, &W2, &LOG, &LOGC, &meta, &flags}) release(*b);
+    }
+};
+
+struct srq_exec {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    int32_t *d_err = nullptr;  // [4] device error words
+    int32_t *h_err = nullptr;  // pinned mirror
+    Workspace ws;
+    int32_t *h_meta = nullptr;  // pinned metadata staging
+    size_t h_meta_n = 0;
+};
+
+struct srq_weight {
+    int fmt = SRQ_F32;
+    int64_t rows = 0, cols = 0;
+    void *values = nullptr;
+    float *scales = nullptr;
+    bool owned = false;
+};
+
+struct Layer {
+    srq_weight qkv, o, gu, down;          // fused storage used by the step
+    srq_weight q, k, v, gate, up;         // views into qkv / gu
+    float *n1 = nullptr, *n2 = nullptr, *bias = nullptr;
+};
+
+struct srq_model {
+    int device = 0;
+    srq_exec *e = nullptr;
+    srq_model_config c{};
+    std::string format;
+    int hd = 0, kvdim = 0;
+    srq_weight embed, output;
+    bool has_output = false;
+    float *final_norm = nullptr;
+    std::vector<Layer> L;
+    float *cos_t = nullptr, *sin_t = nullptr;
+    std::vector<float> h_cos, h_sin;
+    std::vector<void *> allocs;
+    int64_t resident = 0;
+};
+
+struct srq_pool {
+    srq_model *m = nullptr;
+    float *base = nullptr;
+    int32_t max_pages = 0, reserved = 0;
+    int64_t page_elems = 0;
+    std::vector<int32_t> free_list;
+};
+
+struct srq_cache {
+    srq_pool *p = nullptr;
+    int32_t pos = 0, reserve = 0;
+    std::vector<int32_t> pages;
+    bool released = false;
+};
+
+namespace {
+
+struct DeviceGuard {
+    int prev = -1;
+    explicit DeviceGuard(int dev) {
+        if (hipGetDevice(&prev) != hipSuccess) prev = -1;
+        if (prev != dev) (void)hipSetDevice(dev);
+    }
+    ~DeviceGuard() {
+        int cur = -1;
+        if (prev >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev) (void)hipSetDevice(prev);
+    }
+};
+
+int check_err_flag(srq_exec *e, int code, const char *what) {
+    SRQ_HIP(hipMemcpyAsync(e->h_err, e->d_err, sizeof(int32_t) * 4, hipMemcpyDeviceToHost, e->stream));
+    SRQ_HIP(hipStreamSynchronize(e->stream));
+    if (e->h_err[0]) {
+        SRQ_HIP(hipMemsetAsync(e->d_err, 0, sizeof(int32_t) * 4, e->stream));
+        SRQ_HIP(hipStreamSynchronize(e->stream));
+        return fail(code, "%s", what);
+    }
+    return SRQ_OK;
+}
+
+int alloc_weight(srq_model *m, srq_weight &w, int fmt, int64_t rows, int64_t cols) {
+    w.fmt = fmt;
+    w.rows = rows;
+    w.cols = cols;
+    int64_t vb = rows * row_bytes(fmt, cols), sb = fmt == SRQ_F32 ? 0 : rows * groups_of(cols) * 4;
+    if (hipMalloc(&w.values, (size_t)std::max<int64_t>(vb, 16)) != hipSuccess)
+        return fail(SRQ_ENOMEM, "weight allocation (%lld bytes) failed", (long long)vb);
+    m->allocs.push_back(w.values);
+    if (sb) {
+        if (hipMalloc((void **)&w.scales, (size_t)sb) != hipSuccess)
+            return fail(SRQ_ENOMEM, "scale allocation failed");
+        m->allocs.push_back(w.scales);
+    }
+    m->resident += vb + sb;
+    return SRQ_OK;
+}
+
+srq_weight view_rows(const srq_weight &w, int64_t row0, int64_t rows) {
+    srq_weight v;
+    v.fmt = w.fmt;
+    v.rows = rows;
+    v.cols = w.cols;
+    v.values = (uint8_t *)w.values + row0 * row_bytes(w.fmt, w.cols);
+    v.scales = w.scales ? w.scales + row0 * groups_of(w.cols) : nullptr;
+    return v;
+}
+
+int alloc_f32(srq_model *m, float **p, int64_t count) {
+    if (hipMalloc((void **)p, (size_t)std::max<int64_t>(count * 4, 16)) != hipSuccess)
+        return fail(SRQ_ENOMEM, "allocation failed");
+    m->allocs.push_back(*p);
+    m->resident += count * 4;
+    return SRQ_OK;
+}
+
+// Fill a weight from a device source (pack or convert).
+int fill_weight(srq_exec *e, const srq_weight &w, const void *src, int dtype) {
+    if (w.fmt == SRQ_F32) return launch_convert_f32(e->stream, w.rows * w.cols, src, dtype, (float *)w.values, e->d_err);
+    return launch_pack(e->stream, w.fmt, w.rows, w.cols, src, dtype, w.values, w.scales, e->d_err);
+}
+
+RowMeta make_meta(srq_exec *e, srq_model *m, int layer, int32_t pt_stride, const int32_t *pos, const int32_t *sess,
+                  const int32_t *pages, srq_pool *pool) {
+    (void)e;
+    RowMeta r;
+    r.pos = pos;
+    r.sess = sess;
+    r.pages = pages;
+    r.pt_stride = pt_stride;
+    r.kv_pool = pool->base;
+    r.page_elems = pool->page_elems;
+    r.layer = layer;
+    (void)m;
+    return r;
+}
+
+// y[n x w.rows] = x . W^T for n rows through the GEMV (chunks of 8) or the
+// MFMA GEMM (n > 16, K multiple of 32), with optional fused RMSNorm.
+int run_linear(srq_exec *e, Workspace &ws, const srq_weight &w, const float *x, int32_t n, float *y, int64_t y_stride,
+               const float *norm_w, double eps, const float *residual) {
+    if (n > 16 && gemm_ok(w.fmt, w.cols) && !norm_w) {
+        SRQ_CHECK(ensure(ws.flags, sizeof(int32_t) * (size_t)n, e->stream));
+        SRQ_CHECK(launch_wide_scan(e->stream, x, n, w.cols, as<int32_t>(ws.flags)));
+        GemmArgs g{w.fmt, w.values, w.scales, w.rows, w.cols, x, n, y, y_stride, residual};
+        SRQ_CHECK(launch_gemm(e->stream, g, as<int32_t>(ws.flags)));
+        return launch_wide_fix(e->stream, g, as<int32_t>(ws.flags));
+    }
+    const int nb = gemv_max_rows(w.fmt, w.cols);
+    if (nb < 1) return fail(SRQ_EINVAL, "input width %lld exceeds the GEMV staging limit", (long long)w.cols);
+    for (int32_t r0 = 0; r0 < n; r0 += nb) {
+        GemvArgs a{};
+        a.fmt = w.fmt;
+        a.values = w.values;
+        a.scales = w.scales;
+        a.rows = w.rows;
+        a.cols = w.cols;
+        a.x = x + (int64_t)r0 * w.cols;
+        a.n = std::min(nb, n - r0);
+        a.row0 = r0;
+        a.norm_w = norm_w;
+        a.norm_eps = eps;
+        a.y = y + (int64_t)r0 * y_stride;
+        a.y_stride = y_stride;
+        a.epilogue = residual ? EPI_RESID : EPI_PLAIN;
+        a.residual = residual ? residual + (int64_t)r0 * y_stride : nullptr;
+        SRQ_CHECK(launch_gemv(e->stream, a));
+    }
+    return SRQ_OK;
+}
+
+}  // namespace
+
+// ====================================================================== ABI
+extern "C" {
+
+int srq_abi_version(void) { return SRQ_ABI_VERSION; }
+
+const char *srq_last_error(void) { return g_err.c_str(); }
+
+int srq_device_count(int *count) {
+    if (!count) return fail(SRQ_EINVAL, "null count");
+    SRQ_HIP(hipGetDeviceCount(count));
+    return SRQ_OK;
+}
+
+int srq_alloc(int device, size_t bytes, void **dptr) {
+    if (!dptr) return fail(SRQ_EINVAL, "null pointer");
+    DeviceGuard g(device);
+    if (hipMalloc(dptr, std::max<size_t>(bytes, 1)) != hipSuccess) {
+        *dptr = nullptr;
+        return fail(SRQ_ENOMEM, "device allocation of %zu bytes failed", bytes);
+    }
+    return SRQ_OK;
+}
+
+int srq_free(void *dptr) {
+    if (dptr) SRQ_HIP(hipFree(dptr));
+    return SRQ_OK;
+}
+
+static int copy(srq_exec *e, void *dst, const void *src, size_t bytes, hipMemcpyKind kind) {
+    if (!e || (!dst && bytes) || (!src && bytes)) return fail(SRQ_EINVAL, "null pointer");
+    if (!bytes) return SRQ_OK;
+    DeviceGuard g(e->device);
+    SRQ_HIP(hipMemcpyAsync(dst, src, bytes, kind, e->stream));
+    SRQ_HIP(hipStreamSynchronize(e->stream));
+    return SRQ_OK;
+}
+
+int srq_copy_h2d(srq_exec *e, void *dst, const void *src, size_t bytes) {
+    return copy(e, dst, src, bytes, hipMemcpyHostToDevice);
+}
+int srq_copy_d2h(srq_exec *e, void *dst, const void *src, size_t bytes) {
+    return copy(e, dst, src, bytes, hipMemcpyDeviceToHost);
+}
+int srq_copy_d2d(srq_exec *e, void *dst, const void *src, size_t bytes) {
+    return copy(e, dst, src, bytes, hipMemcpyDeviceToDevice);
+}
+
+// ---------------------------------------------------------------- executor
+int srq_exec_create(int device, srq_exec **out) {
+    if (!out) return fail(SRQ_EINVAL, "null out");
+    *out = nullptr;
+    int count = 0;
+    SRQ_HIP(hipGetDeviceCount(&count));
+    if (device < 0 || device >= count) return fail(SRQ_EINVAL, "device %d of %d", device, count);
+    DeviceGuard g(device);
+    SRQ_CHECK(prepare_device(device));
+    srq_exec *e = new srq_exec();
+    e->device = device;
+    if (hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking) != hipSuccess) {
+        delete e;
+        return fail(SRQ_EDEVICE, "stream creation failed");
+    }
+    if (hipMalloc((void **)&e->d_err, sizeof(int32_t) * 4) != hipSuccess ||
+        hipHostMalloc((void **)&e->h_err, sizeof(int32_t) * 4) != hipSuccess) {
+        srq_exec_destroy(e);
+        return fail(SRQ_ENOMEM, "executor allocation failed");
+    }
+    SRQ_HIP(hipMemsetAsync(e->d_err, 0, sizeof(int32_t) * 4, e->stream));
+    SRQ_HIP(hipStreamSynchronize(e->stream));
+    *out = e;
+    return SRQ_OK;
+}
+
+int srq_exec_destroy(srq_exec *e) {
+    if (!e) return SRQ_OK;
+    DeviceGuard g(e->device);
+    if (e->stream) (void)hipStreamSynchronize(e->stream);
+    e->ws.release_all();
+    if (e->d_err) (void)hipFree(e->d_err);
+    if (e->h_err) (void)hipHostFree(e->h_err);
+    if (e->h_meta) (void)hipHostFree(e->h_meta);
+    if (e->stream) (void)hipStreamDestroy(e->stream);
+    delete e;
+    return SRQ_OK;
+}
+
+int srq_exec_synchronize(srq_exec *e) {
+    if (!e) return fail(SRQ_EINVAL, "null executor");
+    DeviceGuard g(e->device);
+    SRQ_HIP(hipStreamSynchronize(e->stream));
+    return SRQ_OK;
+}
+
+void *srq_exec_stream(srq_exec *e) { return e ? (void *)e->stream : nullptr; }
+
+// ----------------------------------------------------------------- packing
+int srq_packed_bytes(srq_format fmt, int64_t rows, int64_t cols, int64_t *values_bytes, int64_t *scales_bytes) {
+    if (rows < 0 || cols < 0 || fmt < SRQ_F32 || fmt > SRQ_Q4) return fail(SRQ_EINVAL, "bad shape or format");
+    if (values_bytes) *values_bytes = rows * row_bytes(fmt, cols);
+    if (scales_bytes) *scales_bytes = fmt == SRQ_F32 ? 0 : rows * groups_of(cols) * 4;
+    return SRQ_OK;
+}
+
+int srq_pack(srq_exec *e, srq_format fmt, int64_t rows, int64_t cols, const void *src, srq_src_dtype dtype,
+             void *values, float *scales) {
+    if (!e || !src || !values || !scales) return fail(SRQ_EINVAL, "null pointer");
+    if (fmt != SRQ_Q8 && fmt != SRQ_Q4) return fail(SRQ_EINVAL, "pack format must be Q8 or Q4");
+    if (rows < 0 || cols < 0 || dtype < SRQ_SRC_F32 || dtype > SRQ_SRC_F16) return fail(SRQ_EINVAL, "bad shape or dtype");
+    DeviceGuard g(e->device);
+    SRQ_CHECK(launch_pack(e->stream, fmt, rows, cols, src, dtype, values, scales, e->d_err));
+    return check_err_flag(e, SRQ_ENONFINITE, "non-finite weight in pack source");
+}
+
+// ----------------------------------------------------------------- weights
+int srq_weight_create(srq_exec *e, srq_format fmt, int64_t rows, int64_t cols, const void *src, srq_src_dtype dtype,
+                      srq_weight **out) {
+    if (!e || !out || !src) return fail(SRQ_EINVAL, "null pointer");
+    *out = nullptr;
+    if (rows <= 0 || cols <= 0 || fmt < SRQ_F32 || fmt > SRQ_Q4 || dtype < SRQ_SRC_F32 || dtype > SRQ_SRC_F16)
+        return fail(SRQ_EINVAL, "bad weight shape, format or dtype");
+    DeviceGuard g(e->device);
+    srq_weight *w = new srq_weight();
+    w->fmt = fmt;
+    w->rows = rows;
+    w->cols = cols;
+    w->owned = true;
+    int64_t vb = rows * row_bytes(fmt, cols), sb = fmt == SRQ_F32 ? 0 : rows * groups_of(cols) * 4;
+    if (hipMalloc(&w->values, (size_t)vb) != hipSuccess || (sb && hipMalloc((void **)&w->scales, (size_t)sb) != hipSuccess)) {
+        srq_weight_destroy(w);
+        return fail(SRQ_ENOMEM, "weight allocation failed");
+    }
+    int rc = fmt == SRQ_F32 ? launch_convert_f32(e->stream, rows * cols, src, dtype, (float *)w->values, e->d_err)
+                            : launch_pack(e->stream, fmt, rows, cols, src, dtype, w->values, w->scales, e->d_err);
+    if (rc == SRQ_OK) rc = check_err_flag(e, SRQ_ENONFINITE, "non-finite weight");
+    if (rc != SRQ_OK) {
+        srq_weight_destroy(w);
+        return rc;
+    }
+    *out = w;
+    return SRQ_OK;
+}
+
+int srq_weight_wrap(srq_format fmt, int64_t rows, int64_t cols, void *values, float *scales, srq_weight **out) {
+    if (!out || !values || (fmt != SRQ_F32 && !scales)) return fail(SRQ_EINVAL, "null pointer");
+    if (rows <= 0 || cols <= 0 || fmt < SRQ_F32 || fmt > SRQ_Q4) return fail(SRQ_EINVAL, "bad weight shape or format");
+    srq_weight *w = new srq_weight();
+    w->fmt = fmt;
+    w->rows = rows;
+    w->cols = cols;
+    w->values = values;
+    w->scales = fmt == SRQ_F32 ? nullptr : scales;
+    w->owned = false;
+    *out = w;
+    return SRQ_OK;
+}
+
+int srq_weight_destroy(srq_weight *w) {
+    if (!w) return SRQ_OK;
+    if (w->owned) {
+        if (w->values) (void)hipFree(w->values);
+        if (w->scales) (void)hipFree(w->scales);
+    }
+    delete w;
+    return SRQ_OK;
+}
+
+int srq_weight_info(const srq_weight *w, int *fmt, int64_t *rows, int64_t *cols, void **values, float **scales) {
+    if (!w) return fail(SRQ_EINVAL, "null weight");
+    if (fmt) *fmt = w->fmt;
+    if (rows) *rows = w->rows;
+    if (cols) *cols = w->cols;
+    if (values) *values = w->values;
+    if (scales) *scales = w->scales;
+    return SRQ_OK;
+}
+
+int srq_dequant_rows(srq_exec *e, const srq_weight *w, const int32_t *rows, int32_t count, float *dst) {
+    if (!e || !w || (count > 0 && (!rows || !dst))) return fail(SRQ_EINVAL, "null pointer");
+    if (count < 0) return fail(SRQ_EINVAL, "negative count");
+    DeviceGuard g(e->device);
+    SRQ_CHECK(launch_dequant_rows(e->stream, w->fmt, w->cols, w->values, w->scales, rows, count, dst));
+    SRQ_HIP(hipStreamSynchronize(e->stream));
+    return SRQ_OK;
+}
+
+// ------------------------------------------------------------------ linear
+int srq_linear(srq_exec *e, float *y, const float *x, const srq_weight *w, int32_t n) {
+    if (!e || !y || !x || !w) return fail(SRQ_EINVAL, "null pointer");
+    if (n < 1 || n > 1024) return fail(SRQ_EINVAL, "linear rows n=%d outside 1..1024", n);
+    const char *yb = (const char *)y, *xb = (const char *)x;
+    if (yb < xb + (size_t)n * w->cols * 4 && xb < yb + (size_t)n * w->rows * 4)
+        return fail(SRQ_EINVAL, "y overlaps x");
+    DeviceGuard g(e->device);
+    SRQ_CHECK(run_linear(e, e->ws, *w, x, n, y, w->rows, nullptr, 0.0, nullptr));
+    SRQ_HIP(hipStreamSynchronize(e->stream));
+    return SRQ_OK;
+}
+
+// ------------------------------------------------------------------- model
+int srq_model_create(srq_exec *e, const srq_model_config *c, const char *weight_format, srq_model **out) {
+    if (!e || !c || !weight_format || !out) return fail(SRQ_EINVAL, "null pointer");
+    *out = nullptr;
+    std::string f(weight_format);
+    if (f != "f32" && f != "q8" && f != "q4" && f != "q4-mixed")
+        return fail(SRQ_EINVAL, "weight-format must be f32, q8, q4 or q4-mixed");
+    if (c->vocab < 1 || c->dim < 2 || c->layers < 1 || c->heads < 1 || c->kv_heads < 1 || c->hidden < 1 ||
+        c->context < 1 || c->context > 32768 || c->dim % c->heads || c->heads % c->kv_heads ||
+        (c->dim / c->heads) % 2 || c->dim / c->heads > 256 || !(c->rope_theta > 1) || !(c->norm_eps >= 1e-12) ||
+        !(c->norm_eps <= 1))
+        return fail(SRQ_EINVAL, "invalid model configuration");
+    DeviceGuard g(e->device);
+    srq_model *m = new srq_model();
+    m->device = e->device;
+    m->e = e;
+    m->c = *c;
+    m->format = f;
+    m->hd = c->dim / c->heads;
+    m->kvdim = m->hd * c->kv_heads;
+    const int fm = matrix_format(f, false), fe = matrix_format(f, true);
+    const int64_t d = c->dim, kd = m->kvdim, H = c->hidden;
+    int rc = alloc_weight(m, m->embed, fe, c->vocab, d);
+    if (rc == SRQ_OK && !c->tied) {
+        rc = alloc_weight(m, m->output, fe, c->vocab, d);
+        m->has_output = true;
+    }
+    if (rc == SRQ_OK) rc = alloc_f32(m, &m->final_norm, d);
+    m->L.resize(c->layers);
+    for (int l = 0; l < c->layers && rc == SRQ_OK; ++l) {
+        Layer &L = m->L[l];
+        rc = alloc_weight(m, L.qkv, fm, d + 2 * kd, d);
+        if (rc == SRQ_OK) rc = alloc_weight(m, L.o, fm, d, d);
+        if (rc == SRQ_OK) rc = alloc_weight(m, L.gu, fm, 2 * H, d);
+        if (rc == SRQ_OK) rc = alloc_weight(m, L.down, fm, d, H);
+        if (rc == SRQ_OK) rc = alloc_f32(m, &L.n1, d);
+        if (rc == SRQ_OK) rc = alloc_f32(m, &L.n2, d);
+        if (rc == SRQ_OK && c->qkv_bias) rc = alloc_f32(m, &L.bias, d + 2 * kd);
+        if (rc == SRQ_OK) {
+            L.q = view_rows(L.qkv, 0, d);
+            L.k = view_rows(L.qkv, d, kd);
+            L.v = view_rows(L.qkv, d + kd, kd);
+            L.gate = view_rows(L.gu, 0, H);
+            L.up = view_rows(L.gu, H, H);
+        }
+    }
+    // RoPE tables (M:5034-5043), computed once on the host as the reference
+    // does at load time, then resident on the device.
+    if (rc == SRQ_OK) {
+        const int half = m->hd / 2;
+        m->h_cos.resize((size_t)c->context * half);
+        m->h_sin.resize((size_t)c->context * half);
+        std::vector<float> inv(half);
+        for (int j = 0; j < half; ++j) inv[j] = inverse_frequency(*c, m->hd, j);
+        for (int p = 0; p < c->context; ++p)
+            for (int j = 0; j < half; ++j) {
+                volatile float prod = (float)p * inv[j];
+                double angle = (double)prod;
+                m->h_cos[(size_t)p * half + j] = (float)std::cos(angle);
+                m->h_sin[(size_t)p * half + j] = (float)std::sin(angle);
+            }
+        const int64_t tbytes = (int64_t)c->context * half * 4;
+        if (hipMalloc((void **)&m->cos_t, tbytes) != hipSuccess || hipMalloc((void **)&m->sin_t, tbytes) != hipSuccess)
+            rc = fail(SRQ_ENOMEM, "RoPE table allocation failed");
+        else {
+            m->allocs.push_back(m->cos_t);
+            m->allocs.push_back(m->sin_t);
+            if (hipMemcpy(m->cos_t, m->h_cos.data(), tbytes, hipMemcpyHostToDevice) != hipSuccess ||
+                hipMemcpy(m->sin_t, m->h_sin.data(), tbytes, hipMemcpyHostToDevice) != hipSuccess)
+                rc = fail(SRQ_EDEVICE, "RoPE table upload failed");
+        }
+    }
+    if (rc != SRQ_OK) {
+        srq_model_destroy(m);
+        return rc;
+    }
+    *out = m;
+    return SRQ_OK;
+}
+
+int srq_model_destroy(srq_model *m) {
+    if (!m) return SRQ_OK;
+    DeviceGuard g(m->device);
+    (void)hipDeviceSynchronize();
+    for (void *p : m->allocs) (void)hipFree(p);
+    delete m;
+    return SRQ_OK;
+}
+
+int srq_model_resident_bytes(const srq_model *m, int64_t *bytes) {
+    if (!m || !bytes) return fail(SRQ_EINVAL, "null pointer");
+    // RoPE tables are not weights: hfWeightLayoutFor counts parameters only.
+    *bytes = m->resident;
+    return SRQ_OK;
+}
+
+static srq_weight *model_matrix(srq_model *m, int kind, int layer) {
+    if (kind == SRQ_T_EMBED) return &m->embed;
+    if (kind == SRQ_T_OUTPUT) return m->has_output ? &m->output : nullptr;
+    if (layer < 0 || layer >= m->c.layers) return nullptr;
+    Layer &L = m->L[layer];
+    switch (kind) {
+        case SRQ_T_Q: return &L.q;
+        case SRQ_T_K: return &L.k;
+        case SRQ_T_V: return &L.v;
+        case SRQ_T_O: return &L.o;
+        case SRQ_T_GATE: return &L.gate;
+        case SRQ_T_UP: return &L.up;
+        case SRQ_T_DOWN: return &L.down;
+    }
+    return nullptr;
+}
+
+int srq_model_weight(srq_model *m, int kind, int layer, srq_weight **out) {
+    if (!m || !out) return fail(SRQ_EINVAL, "null pointer");
+    srq_weight *w = model_matrix(m, kind, layer);
+    if (!w) return fail(SRQ_EINVAL, "no matrix of kind %d at layer %d", kind, layer);
+    *out = w;
+    return SRQ_OK;
+}
+
+int srq_model_load(srq_model *m, int kind, int layer, const void *src, srq_src_dtype dtype) {
+    if (!m || !src) return fail(SRQ_EINVAL, "null pointer");
+    if (dtype < SRQ_SRC_F32 || dtype > SRQ_SRC_F16) return fail(SRQ_EINVAL, "bad source dtype");
+    srq_exec *e = m->e;
+    DeviceGuard g(m->device);
+    const int64_t d = m->c.dim, kd = m->kvdim;
+    int rc;
+    float *vec = nullptr;
+    int64_t count = 0;
+    switch (kind) {
+        case SRQ_T_FINAL_NORM: vec = m->final_norm, count = d; break;
+        case SRQ_T_ATTN_NORM:
+        case SRQ_T_FFN_NORM:
+            if (layer < 0 || layer >= m->c.layers) return fail(SRQ_EINVAL, "layer %d out of range", layer);
+            vec = kind == SRQ_T_ATTN_NORM ? m->L[layer].n1 : m->L[layer].n2;
+            count = d;
+            break;
+        case SRQ_T_Q_BIAS:
+        case SRQ_T_K_BIAS:
+        case SRQ_T_V_BIAS:
+            if (!m->c.qkv_bias) return fail(SRQ_EINVAL, "model has no q/k/v biases");
+            if (layer < 0 || layer >= m->c.layers) return fail(SRQ_EINVAL, "layer %d out of range", layer);
+            vec = m->L[layer].bias + (kind == SRQ_T_Q_BIAS ? 0 : kind == SRQ_T_K_BIAS ? d : d + kd);
+            count = kind == SRQ_T_Q_BIAS ? d : kd;
+            break;
+        default: break;
+    }
+    if (vec) {
+        rc = launch_convert_f32(e->stream, count, src, dtype, vec, e->d_err);
+    } else {
+        srq_weight *w = model_matrix(m, kind, layer);
+        if (!w) return fail(SRQ_EINVAL, "no tensor of kind %d at layer %d", kind, layer);
+        rc = fill_weight(e, *w, src, dtype);
+    }
+    SRQ_CHECK(rc);
+    return check_err_flag(e, SRQ_ENONFINITE, "non-finite HF weight");
+}
+
+int srq_model_rope_tables(const srq_model *m, float *cos_out, float *sin_out) {
+    if (!m || !cos_out || !sin_out) return fail(SRQ_EINVAL, "null pointer");
+    memcpy(cos_out, m->h_cos.data(), m->h_cos.size() * 4);
+    memcpy(sin_out, m->h_sin.data(), m->h_sin.size() * 4);
+    return SRQ_OK;
+}
+
+// -------------------------------------------------------------------- pool
+int srq_pool_create(srq_model *m, int32_t max_pages, srq_pool **out) {
+    if (!m || !out) return fail(SRQ_EINVAL, "null pointer");
+    *out = nullptr;
+    if (max_pages < 1) return fail(SRQ_EINVAL, "pool needs at least one page");
+    DeviceGuard g(m->device);
+    srq_pool *p = new srq_pool();
+    p->m = m;
+    p->max_pages = max_pages;
+    p->page_elems = (int64_t)2 * kPageTokens * m->kvdim * m->c.layers;
+    const size_t bytes = (size_t)max_pages * p->page_elems * 4;
+    if (hipMalloc((void **)&p->base, bytes) != hipSuccess) {
+        delete p;
+        return fail(SRQ_ENOMEM, "KV pool of %zu bytes does not fit", bytes);
+    }
+    if (hipMemset(p->base, 0, bytes) != hipSuccess) {
+        (void)hipFree(p->base);
+        delete p;
+        return fail(SRQ_EDEVICE, "KV pool clear failed");
+    }
+    for (int32_t i = max_pages - 1; i >= 0; --i) p->free_list.push_back(i);
+    *out = p;
+    return SRQ_OK;
+}
+
+int srq_pool_destroy(srq_pool *p) {
+    if (!p) return SRQ_OK;
+    DeviceGuard g(p->m->device);
+    (void)hipDeviceSynchronize();
+    if (p->base) (void)hipFree(p->base);
+    delete p;
+    return SRQ_OK;
+}
+
+int srq_cache_create(srq_pool *p, int32_t reserve_pages, srq_cache **out) {
+    if (!p || !out) return fail(SRQ_EINVAL, "null pointer");
+    *out = nullptr;
+    const int32_t limit = (p->m->c.context + kPageTokens - 1) / kPageTokens;
+    if (reserve_pages < 1 || reserve_pages > limit) return fail(SRQ_EINVAL, "reservation must be 1..%d pages", limit);
+    if (p->reserved + reserve_pages > p->max_pages)
+        return fail(SRQ_ENOSPC, "KV pool reservation exceeded: %d + %d > %d pages", p->reserved, reserve_pages,
+                    p->max_pages);
+    srq_cache *c = new srq_cache();
+    c->p = p;
+    c->reserve = reserve_pages;
+    p->reserved += reserve_pages;
+    *out = c;
+    return SRQ_OK;
+}
+
+int srq_cache_destroy(srq_cache *c) {
+    if (!c) return SRQ_OK;
+    if (!c->released) {
+        for (int32_t pg : c->pages) c->p->free_list.push_back(pg);
+        c->p->reserved -= c->reserve;
+        c->released = true;
+    }
+    delete c;
+    return SRQ_OK;
+}
+
+int srq_cache_pos(const srq_cache *c, int32_t *pos) {
+    if (!c || !pos) return fail(SRQ_EINVAL, "null pointer");
+    *pos = c->pos;
+    return SRQ_OK;
+}
+
+int srq_cache_read(srq_exec *e, const srq_cache *c, int32_t layer, int32_t pos0, int32_t count, float *k, float *v) {
+    if (!e || !c || (count > 0 && (!k || !v))) return fail(SRQ_EINVAL, "null pointer");
+    srq_model *m = c->p->m;
+    if (layer < 0 || layer >= m->c.layers || pos0 < 0 || count < 0 ||
+        (int64_t)pos0 + count > (int64_t)c->pages.size() * kPageTokens)
+        return fail(SRQ_EINVAL, "KV rows outside the cache's pages");
+    DeviceGuard g(e->device);
+    const int64_t kd = m->kvdim;
+    for (int32_t i = 0; i < count; ++i) {
+        const int32_t pos = pos0 + i;
+        const float *base = c->p->base + (int64_t)c->pages[pos / kPageTokens] * c->p->page_elems +
+                            (int64_t)layer * 2 * kPageTokens * kd + (int64_t)(pos % kPageTokens) * kd;
+        SRQ_HIP(hipMemcpyAsync(k + i * kd, base, kd * 4, hipMemcpyDeviceToHost, e->stream));
+        SRQ_HIP(hipMemcpyAsync(v + i * kd, base + kPageTokens * kd, kd * 4, hipMemcpyDeviceToHost, e->stream));
+    }
+    SRQ_HIP(hipStreamSynchronize(e->stream));
+    return SRQ_OK;
+}
+
+}  // extern "C"
+
+// -------------------------------------------------------------------- step
+namespace {
+
+// Validation of prefillSelected (M:6246-6339) without mutating anything.
+int validate_step(srq_model *m, int32_t sessions, srq_cache *const *caches, const int32_t *lens, const int32_t *tokens,
+                  int32_t *n_out, int32_t *max_pos) {
+    if (sessions < 1 || sessions > 256 || !caches || !lens || !tokens)
+        return fail(SRQ_EINVAL, "invalid prefill batch (1..256 sessions)");
+    int32_t n = 0, mp = 0;
+    std::vector<const srq_cache *> seen;
+    std::vector<std::pair<srq_pool *, int32_t>> need;
+    for (int32_t i = 0; i < sessions; ++i) {
+        const srq_cache *c = caches[i];
+        if (!c || c->released || c->p->m != m || std::find(seen.begin(), seen.end(), c) != seen.end())
+            return fail(SRQ_EINVAL, "foreign, stale, released, or duplicate KV cache");
+        seen.push_back(c);
+        const int32_t len = lens[i];
+        if (len < 1 || len > 1024 - n)
+            return fail(SRQ_EINVAL, "prefill requires nonempty chunks totaling at most 1024 tokens");
+        if (c->pos < 0 || c->pos > m->c.context || len > m->c.context - c->pos)
+            return fail(SRQ_ERANGE, "KV cache context exhausted or invalid position");
+        for (int32_t j = 0; j < len; ++j)
+            if (tokens[n + j] < 0 || tokens[n + j] >= m->c.vocab) return fail(SRQ_EINVAL, "token outside vocabulary");
+        const int32_t end = c->pos + len;
+        const int32_t pages = (end + kPageTokens - 1) / kPageTokens;
+        if (pages > c->reserve) return fail(SRQ_ENOSPC, "insufficient KV page reservation");
+        const int32_t extra = std::max<int32_t>(0, pages - (int32_t)c->pages.size());
+        bool found = false;
+        for (auto &pr : need)
+            if (pr.first == c->p) pr.second += extra, found = true;
+        if (!found) need.push_back({c->p, extra});
+        n += len;
+        mp = std::max(mp, end);
+    }
+    for (auto &pr : need)
+        if (pr.second > (int32_t)pr.first->free_list.size()) return fail(SRQ_ENOSPC, "insufficient KV page reservation");
+    *n_out = n;
+    *max_pos = mp;
+    return SRQ_OK;
+}
+
+struct StepMeta {
+    int32_t *tokens, *pos, *sess, *pages, *sel, *expand;
+    int32_t pt_stride;
+};
+
+// Layout of the packed metadata buffer (device and pinned host mirror).
+size_t meta_words(int32_t n, int32_t sessions, int32_t pt_stride) {
+    return (size_t)n * 3 + (size_t)sessions * pt_stride + (size_t)sessions * 2;
+}
+
+StepMeta carve(int32_t *base, int32_t n, int32_t sessions, int32_t pt_stride) {
+    StepMeta s;
+    s.tokens = base;
+    s.pos = base + n;
+    s.sess = base + 2 * n;
+    s.pages = base + 3 * n;
+    s.sel = s.pages + (size_t)sessions * pt_stride;
+    s.expand = s.sel + sessions;
+    s.pt_stride = pt_stride;
+    return s;
+}
+
+int ensure_host_meta(srq_exec *e, size_t words) {
+    if (words <= e->h_meta_n) return SRQ_OK;
+    if (e->h_meta) {
+        SRQ_HIP(hipStreamSynchronize(e->stream));
+        (void)hipHostFree(e->h_meta);
+        e->h_meta = nullptr;
+    }
+    size_t want = std::max<size_t>(words, 4096);
+    if (hipHostMalloc((void **)&e->h_meta, want * 4) != hipSuccess) return fail(SRQ_ENOMEM, "pinned allocation failed");
+    e->h_meta_n = want;
+    return SRQ_OK;
+}
+
+// Enqueue the layers of one step for n rows whose metadata is on device.
+int enqueue_layers(srq_exec *e, Workspace &ws, srq_model *m, srq_pool *pool, int32_t n, int32_t max_len,
+                   const StepMeta &dm, const volatile int32_t *cancel) {
+    const srq_model_config &c = m->c;
+    const int64_t d = c.dim, kd = m->kvdim, H = c.hidden;
+    float *X = as<float>(ws.X), *N = as<float>(ws.N), *Q = as<float>(ws.Q), *A = as<float>(ws.A);
+    float *Hh = as<float>(ws.H), *W2 = as<float>(ws.W2);
+    const bool use_gemm = n > 16 && gemm_ok(m->L[0].qkv.fmt, d) && gemm_ok(m->L[0].down.fmt, H);
+    for (int l = 0; l < c.layers; ++l) {
+        if (cancel && *cancel) return fail(SRQ_ECANCELED, "context canceled");
+        Layer &L = m->L[l];
+        RowMeta meta = make_meta(e, m, l, dm.pt_stride, dm.pos, dm.sess, dm.pages, pool);
+        const int nbd = gemv_max_rows(L.qkv.fmt, d);
+        if (nbd < 1) return fail(SRQ_EINVAL, "model width %lld exceeds the GEMV staging limit", (long long)d);
+        if (!use_gemm) {
+            for (int32_t r0 = 0; r0 < n; r0 += nbd) {
+                GemvArgs a{};
+                a.fmt = L.qkv.fmt;
+                a.values = L.qkv.values;
+                a.scales = L.qkv.scales;
+                a.rows = L.qkv.rows;
+                a.cols = d;
+                a.x = X + r0 * d;
+                a.n = std::min(nbd, n - r0);
+                a.row0 = r0;
+                a.norm_w = L.n1;
+                a.norm_eps = c.norm_eps;
+                a.y = Q + r0 * d;
+                a.y_stride = d;
+                a.epilogue = EPI_ROPE_KV;
+                a.dim = (int32_t)d;
+                a.kvdim = (int32_t)kd;
+                a.head_dim = m->hd;
+                a.cos_t = m->cos_t;
+                a.sin_t = m->sin_t;
+                a.bias = L.bias;
+                a.meta = meta;
+                SRQ_CHECK(launch_gemv(e->stream, a));
+            }
+        } else {
+            SRQ_CHECK(launch_rmsnorm(e->stream, X, L.n1, N, n, (int32_t)d, c.norm_eps));
+            SRQ_CHECK(run_linear(e, ws, L.qkv, N, n, W2, d + 2 * kd, nullptr, 0.0, nullptr));
+            SRQ_CHECK(launch_rope_kv(e->stream, W2, L.bias, n, (int32_t)d, (int32_t)kd, m->hd, m->cos_t, m->sin_t, Q, meta));
+        }
+        AttnArgs at{};
+        at.q = Q;
+        at.out = A;
+        at.n = n;
+        at.heads = c.heads;
+        at.kv_heads = c.kv_heads;
+        at.head_dim = m->hd;
+        at.max_len = max_len;
+        at.meta = meta;
+        SRQ_CHECK(launch_attention(e->stream, at));
+        // O projection + residual (M:6398-6400).
+        SRQ_CHECK(run_linear(e, ws, L.o, A, n, X, d, nullptr, 0.0, X));
+        if (!use_gemm) {
+            for (int32_t r0 = 0; r0 < n; r0 += nbd) {
+                GemvArgs a{};
+                a.fmt = L.gu.fmt;
+                a.values = L.gu.values;
+                a.scales = L.gu.scales;
+                a.rows = 2 * H;
+                a.cols = d;
+                a.x = X + r0 * d;
+                a.n = std::min(nbd, n - r0);
+                a.row0 = r0;
+                a.norm_w = L.n2;
+                a.norm_eps = c.norm_eps;
+                a.y = Hh + r0 * H;
+                a.y_stride = H;
+                a.epilogue = EPI_SWIGLU;
+                SRQ_CHECK(launch_gemv(e->stream, a));
+            }
+        } else {
+            SRQ_CHECK(launch_rmsnorm(e->stream, X, L.n2, N, n, (int32_t)d, c.norm_eps));
+            SRQ_CHECK(run_linear(e, ws, L.gu, N, n, W2, 2 * H, nullptr, 0.0, nullptr));
+            SRQ_CHECK(launch_swiglu(e->stream, W2, n, (int32_t)H, Hh));
+        }
+        // down + residual (M:6415-6417).
+        SRQ_CHECK(run_linear(e, ws, L.down, Hh, n, X, d, nullptr, 0.0, X));
+    }
+    return SRQ_OK;
+}
+
+// Final norm + head on `heads` compacted rows (already in T) -> LOGC.
+int enqueue_head(srq_exec *e, Workspace &ws, srq_model *m, const float *rows, int32_t heads) {
+    const srq_weight &head = m->has_output ? m->output : m->embed;
+    float *N = as<float>(ws.N), *LOGC = as<float>(ws.LOGC);
+    if (heads > 16 && gemm_ok(head.fmt, m->c.dim)) {
+        SRQ_CHECK(launch_rmsnorm(e->stream, rows, m->final_norm, N, heads, m->c.dim, m->c.norm_eps));
+        return run_linear(e, ws, head, N, heads, LOGC, m->c.vocab, nullptr, 0.0, nullptr);
+    }
+    return run_linear(e, ws, head, rows, heads, LOGC, m->c.vocab, m->final_norm, m->c.norm_eps, nullptr);
+}
+
+int ensure_workspace(srq_exec *e, Workspace &ws, srq_model *m, int32_t n, int32_t sessions) {
+    const int64_t d = m->c.dim, kd = m->kvdim, H = m->c.hidden, V = m->c.vocab;
+    const size_t nd = (size_t)n * d * 4;
+    SRQ_CHECK(ensure(ws.X, nd, e->stream));
+    SRQ_CHECK(ensure(ws.N, nd, e->stream));
+    SRQ_CHECK(ensure(ws.Q, nd, e->stream));
+    SRQ_CHECK(ensure(ws.A, nd, e->stream));
+    SRQ_CHECK(ensure(ws.T, (size_t)std::max<int64_t>(n, sessions) * d * 4, e->stream));
+    SRQ_CHECK(ensure(ws.H, (size_t)n * H * 4, e->stream));
+    SRQ_CHECK(ensure(ws.W2, (size_t)n * std::max<int64_t>(d + 2 * kd, 2 * H) * 4, e->stream));
+    SRQ_CHECK(ensure(ws.LOGC, (size_t)sessions * V * 4, e->stream));
+    SRQ_CHECK(ensure(ws.LOG, (size_t)sessions * V * 4, e->stream));
+    return SRQ_OK;
+}
+
+}  // namespace
+
+extern "C" int srq_step(srq_exec *e, srq_model *m, int32_t sessions, srq_cache *const *caches,
+                        const int32_t *chunk_lens, const int32_t *tokens, const uint8_t *want, float **logits,
+                        float *logits_host, const volatile int32_t *cancel) {
+    if (!e || !m) return fail(SRQ_EINVAL, "null executor or model");
+    if (logits) *logits = nullptr;
+    if (cancel && *cancel) return fail(SRQ_ECANCELED, "context canceled");
+    int32_t n = 0, max_pos = 0;
+    SRQ_CHECK(validate_step(m, sessions, caches, chunk_lens, tokens, &n, &max_pos));
+    DeviceGuard g(e->device);
+    srq_pool *pool = caches[0]->p;
+    for (int32_t i = 1; i < sessions; ++i)
+        if (caches[i]->p != pool) return fail(SRQ_EINVAL, "sessions of one step must share a KV pool");
+    Workspace &ws = e->ws;
+    SRQ_CHECK(ensure_workspace(e, ws, m, n, sessions));
+    const int32_t pt_stride = (m->c.context + kPageTokens - 1) / kPageTokens;
+    const size_t words = meta_words(n, sessions, pt_stride);
+    SRQ_CHECK(ensure(ws.meta, words * 4, e->stream));
+    SRQ_CHECK(ensure_host_meta(e, words));
+    SRQ_HIP(hipStreamSynchronize(e->stream));  // the pinned staging may still feed a copy
+
+    // Acquire pages (validation proved they exist), then fill metadata.
+    for (int32_t i = 0; i < sessions; ++i) {
+        srq_cache *c = caches[i];
+        const int32_t pages = (c->pos + chunk_lens[i] + kPageTokens - 1) / kPageTokens;
+        while ((int32_t)c->pages.size() < pages) {
+            c->pages.push_back(pool->free_list.back());
+            pool->free_list.pop_back();
+        }
+    }
+    StepMeta hm = carve(e->h_meta, n, sessions, pt_stride);
+    std::vector<int32_t> last_rows(sessions);
+    int32_t r = 0;
+    for (int32_t i = 0; i < sessions; ++i) {
+        for (int32_t j = 0; j < chunk_lens[i]; ++j, ++r) {
+            hm.tokens[r] = tokens[r];
+            hm.pos[r] = caches[i]->pos + j;
+            hm.sess[r] = i;
+        }
+        last_rows[i] = r - 1;
+        int32_t *pt = hm.pages + (size_t)i * pt_stride;
+        for (int32_t p = 0; p < pt_stride; ++p) pt[p] = p < (int32_t)caches[i]->pages.size() ? caches[i]->pages[p] : 0;
+    }
+    int32_t heads = 0;
+    for (int32_t i = 0; i < sessions; ++i) {
+        if (!want || want[i]) {
+            hm.sel[heads] = last_rows[i];
+            hm.expand[i] = heads++;
+        } else {
+            hm.expand[i] = -1;
+        }
+    }
+    SRQ_HIP(hipMemcpyAsync(ws.meta.p, e->h_meta, words * 4, hipMemcpyHostToDevice, e->stream));
+    StepMeta dm = carve(as<int32_t>(ws.meta), n, sessions, pt_stride);
+
+    // Embedding rows (copyRow, M:6364-6375).
+    SRQ_CHECK(launch_dequant_rows(e->stream, m->embed.fmt, m->c.dim, m->embed.values, m->embed.scales, dm.tokens, n,
+                                  as<float>(ws.X)));
+    int rc = enqueue_layers(e, ws, m, pool, n, max_pos, dm, cancel);
+    if (rc == SRQ_OK && heads > 0) {
+        rc = launch_gather_rows(e->stream, as<float>(ws.X), m->c.dim, dm.sel, heads, as<float>(ws.T));
+        if (rc == SRQ_OK) rc = enqueue_head(e, ws, m, as<float>(ws.T), heads);
+    }
+    float *out = as<float>(ws.LOGC);
+    if (rc == SRQ_OK && want) {
+        rc = launch_gather_rows(e->stream, as<float>(ws.LOGC), m->c.vocab, dm.expand, sessions, as<float>(ws.LOG));
+        out = as<float>(ws.LOG);
+    }
+    hipError_t he = hipStreamSynchronize(e->stream);
+    if (rc != SRQ_OK) return rc;
+    if (he != hipSuccess) return fail(SRQ_EDEVICE, "step failed: %s", hipGetErrorString(he));
+    if (cancel && *cancel) return fail(SRQ_ECANCELED, "context canceled");
+    if (logits_host)
+        SRQ_HIP(hipMemcpy(logits_host, out, (size_t)sessions * m->c.vocab * 4, hipMemcpyDeviceToHost));
+    for (int32_t i = 0; i < sessions; ++i) caches[i]->pos += chunk_lens[i];
+    if (logits) *logits = out;
+    return SRQ_OK;
+}
+
+extern "C" int srq_argmax(srq_exec *e, const float *logits, int32_t rows, int32_t vocab, int32_t *ids) {
+    if (!e || !logits || !ids) return fail(SRQ_EINVAL, "null pointer");
+    if (rows < 1 || vocab < 1) return fail(SRQ_EINVAL, "empty logits");
+    DeviceGuard g(e->device);
+    SRQ_CHECK(ensure(e->ws.flags, sizeof(int32_t) * (size_t)rows, e->stream));
+    SRQ_CHECK(launch_argmax(e->stream, logits, rows, vocab, as<int32_t>(e->ws.flags), e->d_err));
+    SRQ_HIP(hipMemcpyAsync(ids, e->ws.flags.p, sizeof(int32_t) * rows, hipMemcpyDeviceToHost, e->stream));
+    return check_err_flag(e, SRQ_ENONFINITE, "non-finite HF logits");
+}
+
+// ----------------------------------------------------------- greedy decoder
+struct srq_decoder {
+    srq_exec *e = nullptr;
+    srq_model *m = nullptr;
+    srq_cache *c = nullptr;
+    int32_t start_pos = 0, max_steps = 0, steps = 0;
+    int32_t *dbuf = nullptr;  // pos, sess, counter, embed_id, token, err, pages[pt], out[max]
+    int32_t pt_stride = 0;
+    Workspace ws;             // private: the captured graph points into it
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+};
+
+extern "C" {
+
+int srq_decoder_destroy(srq_decoder *d);
+
+int srq_decoder_create(srq_exec *e, srq_model *m, srq_cache *c, int32_t first_token, int32_t max_steps,
+                       srq_decoder **out) {
+    if (!e || !m || !c || !out) return fail(SRQ_EINVAL, "null pointer");
+    *out = nullptr;
+    if (c->released || c->p->m != m) return fail(SRQ_EINVAL, "foreign or released KV cache");
+    if (first_token < 0 || first_token >= m->c.vocab) return fail(SRQ_EINVAL, "token outside vocabulary");
+    if (max_steps < 1 || max_steps > m->c.context - c->pos) return fail(SRQ_ERANGE, "KV cache context exhausted");
+    const int32_t end = c->pos + max_steps;
+    const int32_t pages = (end + kPageTokens - 1) / kPageTokens;
+    if (pages > c->reserve || pages - (int32_t)c->pages.size() > (int32_t)c->p->free_list.size())
+        return fail(SRQ_ENOSPC, "insufficient KV page reservation");
+    DeviceGuard g(e->device);
+    srq_decoder *d = new srq_decoder();
+    d->e = e;
+    d->m = m;
+    d->c = c;
+    d->start_pos = c->pos;
+    d->max_steps = max_steps;
+    d->pt_stride = (m->c.context + kPageTokens - 1) / kPageTokens;
+    while ((int32_t)c->pages.size() < pages) {
+        c->pages.push_back(c->p->free_list.back());
+        c->p->free_list.pop_back();
+    }
+    const size_t words = 6 + (size_t)d->pt_stride + (size_t)max_steps;
+    if (hipMalloc((void **)&d->dbuf, words * 4) != hipSuccess) {
+        delete d;
+        return fail(SRQ_ENOMEM, "decoder allocation failed");
+    }
+    std::vector<int32_t> h(words, 0);
+    h[0] = c->pos;
+    h[1] = 0;
+    h[2] = 0;
+    h[3] = first_token;
+    for (int32_t p = 0; p < d->pt_stride; ++p) h[6 + p] = p < (int32_t)c->pages.size() ? c->pages[p] : 0;
+    int rc = ensure_workspace(e, d->ws, m, 1, 1);
+    if (rc == SRQ_OK && hipMemcpy(d->dbuf, h.data(), words * 4, hipMemcpyHostToDevice) != hipSuccess)
+        rc = fail(SRQ_EDEVICE, "decoder upload failed");
+    if (rc == SRQ_OK && hipStreamSynchronize(e->stream) != hipSuccess) rc = fail(SRQ_EDEVICE, "sync failed");
+    if (rc != SRQ_OK) {
+        srq_decoder_destroy(d);
+        return rc;
+    }
+    // One decode step, captured once and replayed: embed -> layers -> final
+    // norm + head -> argmax -> record token, advance position.
+    StepMeta dm{};
+    int32_t *pos = d->dbuf, *sess = d->dbuf + 1, *counter = d->dbuf + 2, *embed_id = d->dbuf + 3;
+    int32_t *token = d->dbuf + 4, *err = d->dbuf + 5, *pt = d->dbuf + 6, *outbuf = d->dbuf + 6 + d->pt_stride;
+    dm.pos = pos;
+    dm.sess = sess;
+    dm.pages = pt;
+    dm.pt_stride = d->pt_stride;
+    if (hipStreamBeginCapture(e->stream, hipStreamCaptureModeThreadLocal) != hipSuccess) {
+        srq_decoder_destroy(d);
+        return fail(SRQ_EDEVICE, "graph capture failed to start");
+    }
+    Workspace &ws = d->ws;
+    rc = launch_dequant_rows(e->stream, m->embed.fmt, m->c.dim, m->embed.values, m->embed.scales, embed_id, 1,
+                             as<float>(ws.X));
+    if (rc == SRQ_OK) rc = enqueue_layers(e, ws, m, c->p, 1, end, dm, nullptr);
+    if (rc == SRQ_OK) rc = enqueue_head(e, ws, m, as<float>(ws.X), 1);
+    if (rc == SRQ_OK) rc = launch_argmax(e->stream, as<float>(ws.LOGC), 1, m->c.vocab, token, err);
+    if (rc == SRQ_OK) rc = launch_advance(e->stream, pos, token, outbuf, counter, embed_id);
+    hipError_t ce = hipStreamEndCapture(e->stream, &d->graph);
+    if (rc == SRQ_OK && ce != hipSuccess) rc = fail(SRQ_EDEVICE, "graph capture failed: %s", hipGetErrorString(ce));
+    if (rc == SRQ_OK && hipGraphInstantiate(&d->exec, d->graph, nullptr, nullptr, 0) != hipSuccess)
+        rc = fail(SRQ_EDEVICE, "graph instantiation failed");
+    if (rc != SRQ_OK) {
+        srq_decoder_destroy(d);
+        return rc;
+    }
+    *out = d;
+    return SRQ_OK;
+}
+
+// Enqueue `steps` decode steps (asynchronous; join with srq_exec_synchronize
+// or srq_decoder_tokens).
+int srq_decoder_run(srq_decoder *d, int32_t steps) {
+    if (!d) return fail(SRQ_EINVAL, "null decoder");
+    if (steps < 0 || d->steps + steps > d->max_steps) return fail(SRQ_ERANGE, "decoder step budget exceeded");
+    DeviceGuard g(d->e->device);
+    for (int32_t i = 0; i < steps; ++i) SRQ_HIP(hipGraphLaunch(d->exec, d->e->stream));
+    d->steps += steps;
+    return SRQ_OK;
+}
+
+// Join, copy the tokens produced so far and commit the cache position.
+int srq_decoder_tokens(srq_decoder *d, int32_t *out, int32_t *count) {
+    if (!d || !count) return fail(SRQ_EINVAL, "null pointer");
+    DeviceGuard g(d->e->device);
+    SRQ_HIP(hipStreamSynchronize(d->e->stream));
+    int32_t err = 0;
+    SRQ_HIP(hipMemcpy(&err, d->dbuf + 5, 4, hipMemcpyDeviceToHost));
+    if (out && d->steps)
+        SRQ_HIP(hipMemcpy(out, d->dbuf + 6 + d->pt_stride, (size_t)d->steps * 4, hipMemcpyDeviceToHost));
+    *count = d->steps;
+    d->c->pos = d->start_pos + d->steps;
+    if (err) return fail(SRQ_ENONFINITE, "non-finite HF logits");
+    return SRQ_OK;
+}
+
+int srq_decoder_destroy(srq_decoder *d) {
+    if (!d) return SRQ_OK;
+    DeviceGuard g(d->e->device);
+    (void)hipStreamSynchronize(d->e->stream);
+    if (d->exec) (void)hipGraphExecDestroy(d->exec);
+    if (d->graph) (void)hipGraphDestroy(d->graph);
+    if (d->dbuf) (void)hipFree(d->dbuf);
+    d->ws.release_all();
+    delete d;
+    return SRQ_OK;
+}
+
+int srq_generate_greedy(srq_exec *e, srq_model *m, srq_cache *c, const int32_t *ids, int32_t n_ids, int32_t chunk,
+                        int32_t count, int32_t eos, int32_t *out_tokens, int32_t *produced) {
+    if (!e || !m || !c || !ids || !out_tokens || !produced) return fail(SRQ_EINVAL, "null pointer");
+    *produced = 0;
+    if (n_ids < 1 || count < 1 || count > 256 || chunk < 1 || chunk > 1024 || n_ids > m->c.context - count - c->pos)
+        return fail(SRQ_EINVAL, "invalid HF probe: nonempty IDs, 1..256 outputs, 1..1024 chunk, total within context");
+    for (int32_t i = 0; i < n_ids; ++i)
+        if (ids[i] < 0 || ids[i] >= m->c.vocab) return fail(SRQ_EINVAL, "HF token ID outside vocabulary");
+    float *logits = nullptr;
+    for (int32_t lo = 0; lo < n_ids; lo += chunk) {
+        int32_t len = std::min(chunk, n_ids - lo);
+        srq_cache *cs[1] = {c};
+        SRQ_CHECK(srq_step(e, m, 1, cs, &len, ids + lo, nullptr, &logits, nullptr, nullptr));
+    }
+    int32_t first = 0;
+    SRQ_CHECK(srq_argmax(e, logits, 1, m->c.vocab, &first));
+    out_tokens[0] = first;
+    *produced = 1;
+    if (count == 1 || first == eos) return SRQ_OK;
+    srq_decoder *d = nullptr;
+    SRQ_CHECK(srq_decoder_create(e, m, c, first, count - 1, &d));
+    int rc = SRQ_OK;
+    int32_t done = 0;
+    const int32_t seg = eos >= 0 ? 16 : count - 1;
+    while (rc == SRQ_OK && done < count - 1) {
+        const int32_t k = std::min(seg, count - 1 - done);
+        rc = srq_decoder_run(d, k);
+        int32_t got = 0;
+        if (rc == SRQ_OK) rc = srq_decoder_tokens(d, out_tokens + 1, &got);
+        if (rc != SRQ_OK) break;
+        done = got;
+        bool stop = false;
+        if (eos >= 0)
+            for (int32_t i = 0; i < got; ++i)
+                if (out_tokens[1 + i] == eos) {
+                    // Tokens after the EOS step are not produced; the EOS
+                    // token itself is never decoded (M:1224-1232).
+                    done = i + 1;
+                    c->pos = d->start_pos + i + 1;
+                    stop = true;
+                    break;
+                }
+        *produced = 1 + done;
+        if (stop) break;
+    }
+    srq_decoder_destroy(d);
+    return rc;
+}
+
+}  // extern "C"

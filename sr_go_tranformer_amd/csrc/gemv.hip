@@ -1,0 +1,512 @@
+// Dequant-fused GEMV for decode and small batches (n <= 8 per launch).
+//
+// Counterpart of linearQ8Into / linearQ4Into / linearFP32Range
+// (cmd/monolith/monolith.go M:3942-4780) for batch rows 1..8, with the
+// step's neighbouring glue fused in: RMSNorm of the input (rmsInto,
+// M:6182-6194) as a prologue; RoPE + KV page write (M:6386-6396), SwiGLU
+// (M:6411-6413) or the residual add (M:6400, M:6417) as epilogues.
+//
+// Layout and mapping (HBM-bound; gfx950 wave64):
+//  - A workgroup of 4 waves first stages its n activation rows into LDS
+//    (one read of x per workgroup), optionally normalising them.
+//  - Each wave owns whole output rows, two at a time ("row groups"): its
+//    64 lanes sweep the row in chunks, each lane loading 16 contiguous bytes
+//    per row per chunk (global_load_dwordx4), so a wave reads 1 KiB of a row
+//    per instruction.  Q8: 16 weights / lane / chunk; Q4: 32; F32: 4.
+//  - LDS holds x permuted so that the 16 B a lane reads for its columns are
+//    consecutive across lanes (conflict-free ds_read_b128).
+//  - Q8 codes convert with one SDWA sign-extending v_cvt_f32_i32 each, then
+//    one FMA per weight and batch row.  Q4 nibbles are shifted into the high
+//    half of each byte, which sign-extends to 16*code exactly; the factor 16
+//    is removed exactly after the block partial.
+//  - Per lane: partial over its 16/32 weights of one 64-column block, then
+//    acc = fma(partial, scale, acc); lanes are combined by a fixed xor tree.
+//    The arithmetic of a (row, output) pair never depends on n or on the
+//    row's slot, so results are batch invariant and deterministic.
+//  - Rows holding any |x| > f32(MaxFloat32/(2*64*127)) are recomputed in
+//    FP64 (Sum_g f64(scale_g) * Sum_j f64(x_j) f64(w_j), M:4356-4382).
+#include "srq_internal.h"
+
+namespace srq {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / 64;
+
+template <int FMT, bool FAST>
+struct Lay {
+    static constexpr int E = 4;     // weights per lane per chunk
+    static constexpr int CW = 256;  // columns per wave chunk
+};
+template <>
+struct Lay<SRQ_Q8, true> {
+    static constexpr int E = 16, CW = 1024;
+};
+template <>
+struct Lay<SRQ_Q4, true> {
+    static constexpr int E = 32, CW = 2048;
+};
+template <>
+struct Lay<SRQ_F32, true> {
+    static constexpr int E = 4, CW = 256;
+};
+
+// LDS word of column c: within a chunk, lane l's group q of 4 columns
+// (columns E*l + 4q .. +3) lives at q*256 + 4*l.
+template <int E, int CW>
+__device__ __forceinline__ int xidx(int c) {
+    int ch = c / CW, w = c - ch * CW;
+    int l = w / E, rem = w - l * E;
+    return ch * CW + (rem >> 2) * 256 + l * 4 + (rem & 3);
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+__device__ __forceinline__ double wave_sum_d(double v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+__device__ __forceinline__ float sext8(uint32_t w, int byte) { return (float)(int32_t)(int8_t)(w >> (8 * byte)); }
+
+// Decode one lane's weights of one chunk for the FAST layouts.  Q4 yields
+// 16*code (see header comment).
+template <int FMT>
+__device__ __forceinline__ void decode16(const uint4 raw, float *w) {
+    const uint32_t d[4] = {raw.x, raw.y, raw.z, raw.w};
+    if constexpr (FMT == SRQ_Q8) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            w[4 * k + 0] = sext8(d[k], 0);
+            w[4 * k + 1] = sext8(d[k], 1);
+            w[4 * k + 2] = sext8(d[k], 2);
+            w[4 * k + 3] = sext8(d[k], 3);
+        }
+    } else if constexpr (FMT == SRQ_Q4) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            uint32_t lo = (d[k] << 4) & 0xF0F0F0F0u;  // even columns, *16
+            uint32_t hi = d[k] & 0xF0F0F0F0u;         // odd columns, *16
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                w[8 * k + 2 * b] = sext8(lo, b);
+                w[8 * k + 2 * b + 1] = sext8(hi, b);
+            }
+        }
+    } else {
+        w[0] = __uint_as_float(raw.x);
+        w[1] = __uint_as_float(raw.y);
+        w[2] = __uint_as_float(raw.z);
+        w[3] = __uint_as_float(raw.w);
+    }
+}
+
+// One weight (generic layout, any width).
+template <int FMT>
+__device__ __forceinline__ float weight_at(const uint8_t *wrow, int64_t c) {
+    if constexpr (FMT == SRQ_Q8) return (float)((const int8_t *)wrow)[c];
+    if constexpr (FMT == SRQ_Q4) {
+        uint32_t b = wrow[c >> 1];
+        uint32_t nib = (c & 1) ? (b >> 4) : (b & 15u);
+        return (float)(((int32_t)(nib << 28)) >> 28);
+    }
+    return ((const float *)wrow)[c];
+}
+
+struct Smem {
+    double ss[8][kWaves];
+    float a[8];
+    int wide[8];
+    int any_wide;
+};
+
+template <int FMT, bool FAST, int NB, int EPI>
+__global__ __launch_bounds__(kThreads) void gemv_kernel(const GemvArgs A) {
+    using L = Lay<FMT, FAST>;
+    constexpr int E = L::E, CW = L::CW;
+    extern __shared__ float xs[];
+    __shared__ Smem sm;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int64_t cols = A.cols;
+    const int nch = (int)((cols + CW - 1) / CW);
+    const int ld = nch * CW;  // LDS words per activation row
+
+    // ---- stage x (and RMSNorm) ------------------------------------------
+    if (tid < NB) sm.wide[tid] = 0;
+    if (tid == 0) sm.any_wide = 0;
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+        double ss = 0.0;
+        const float *xb = A.x + (int64_t)b * cols;
+        for (int c = tid; c < ld; c += kThreads) {
+            float v = (b < A.n && c < cols) ? xb[c] : 0.0f;
+            xs[b * ld + xidx<E, CW>(c)] = v;
+            ss += (double)v * (double)v;
+        }
+        if (A.norm_w) {
+            ss = wave_sum_d(ss);
+            if (lane == 0) sm.ss[b][wave] = ss;
+        }
+    }
+    __syncthreads();
+    if (A.norm_w) {
+        if (tid < NB) {
+            double ss = 0.0;
+            for (int w = 0; w < kWaves; ++w) ss += sm.ss[tid][w];
+            sm.a[tid] = (float)(1.0 / sqrt(ss / (double)cols + A.norm_eps));
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+        const float a = A.norm_w ? sm.a[b] : 1.0f;
+        int wide = 0;
+        for (int c = tid; c < cols; c += kThreads) {
+            const int i = b * ld + xidx<E, CW>(c);
+            float v = xs[i];
+            if (A.norm_w) {
+                v = __fmul_rn(__fmul_rn(v, a), A.norm_w[c]);  // (x*a)*w, M:6191
+                xs[i] = v;
+            }
+            wide |= fabsf(v) > kWideLimit;
+        }
+        if (wide && b < A.n) {
+            sm.wide[b] = 1;
+            sm.any_wide = 1;
+        }
+    }
+    __syncthreads();
+
+    // ---- row groups ------------------------------------------------------
+    const int64_t rows = A.rows;
+    const int64_t rb = row_bytes(FMT, cols);
+    const int64_t groups = groups_of(cols);
+    int64_t ngroups;
+    if constexpr (EPI == EPI_SWIGLU)
+        ngroups = rows / 2;
+    else
+        ngroups = (rows + 1) / 2;
+    const int64_t stride = (int64_t)gridDim.x * kWaves;
+    const uint8_t *W = (const uint8_t *)A.values;
+
+    for (int64_t g = (int64_t)blockIdx.x * kWaves + wave; g < ngroups; g += stride) {
+        int64_t r0, r1;
+        if constexpr (EPI == EPI_SWIGLU) {
+            r0 = g;
+            r1 = g + rows / 2;
+        } else if constexpr (EPI == EPI_ROPE_KV) {
+            const int half = A.head_dim / 2;
+            const int64_t qk_pairs = (int64_t)(A.dim + A.kvdim) / 2;
+            if (g < qk_pairs) {
+                const int64_t h = g / half, j = g - h * half;
+                r0 = h * A.head_dim + j;  // heads of q then k are contiguous
+                r1 = r0 + half;
+            } else {
+                r0 = (int64_t)A.dim + A.kvdim + 2 * (g - qk_pairs);
+                r1 = r0 + 1;
+            }
+        } else {
+            r0 = 2 * g;
+            r1 = 2 * g + 1;
+        }
+        const bool has1 = r1 < rows;
+        const uint8_t *w0 = W + r0 * rb;
+        const uint8_t *w1 = W + (has1 ? r1 : r0) * rb;
+        const float *s0 = A.scales ? A.scales + r0 * groups : nullptr;
+        const float *s1 = A.scales ? A.scales + (has1 ? r1 : r0) * groups : nullptr;
+
+        float acc0[NB], acc1[NB];
+#pragma unroll
+        for (int b = 0; b < NB; ++b) acc0[b] = acc1[b] = 0.0f;
+
+        for (int ch = 0; ch < nch; ++ch) {
+            if constexpr (FAST) {
+                const int64_t c0 = (int64_t)ch * CW + (int64_t)lane * E;
+                if (c0 < cols) {
+                    constexpr int BYTES = 16;
+                    const int64_t boff = FMT == SRQ_Q8 ? c0 : FMT == SRQ_Q4 ? c0 / 2 : c0 * 4;
+                    (void)BYTES;
+                    const uint4 raw0 = ld_stream16(w0 + boff);
+                    const uint4 raw1 = ld_stream16(w1 + boff);
+                    float sc0 = 1.0f, sc1 = 1.0f;
+                    if constexpr (FMT != SRQ_F32) {
+                        sc0 = s0[c0 / kBlock];
+                        sc1 = s1[c0 / kBlock];
+                    }
+                    float wv0[E], wv1[E];
+                    if constexpr (FMT == SRQ_F32) {
+                        decode16<FMT>(raw0, wv0);
+                        decode16<FMT>(raw1, wv1);
+                    } else {
+                        // Q4 decodes 32 weights from its 16 bytes.
+                        decode16<FMT>(raw0, wv0);
+                        decode16<FMT>(raw1, wv1);
+                    }
+#pragma unroll
+                    for (int b = 0; b < NB; ++b) {
+                        const float *xb = xs + b * ld + ch * CW + lane * 4;
+                        float p0 = 0.0f, p1 = 0.0f;
+#pragma unroll
+                        for (int q = 0; q < E / 4; ++q) {
+                            const float4 xv = *(const float4 *)(xb + q * 256);
+                            p0 = __builtin_fmaf(xv.x, wv0[4 * q + 0], p0);
+                            p0 = __builtin_fmaf(xv.y, wv0[4 * q + 1], p0);
+                            p0 = __builtin_fmaf(xv.z, wv0[4 * q + 2], p0);
+                            p0 = __builtin_fmaf(xv.w, wv0[4 * q + 3], p0);
+                            p1 = __builtin_fmaf(xv.x, wv1[4 * q + 0], p1);
+                            p1 = __builtin_fmaf(xv.y, wv1[4 * q + 1], p1);
+                            p1 = __builtin_fmaf(xv.z, wv1[4 * q + 2], p1);
+                            p1 = __builtin_fmaf(xv.w, wv1[4 * q + 3], p1);
+                        }
+                        if constexpr (FMT == SRQ_Q4) {
+                            p0 *= 0.0625f;  // exact: undo the *16 of the nibble decode
+                            p1 *= 0.0625f;
+                        }
+                        if constexpr (FMT == SRQ_F32) {
+                            acc0[b] += p0;
+                            acc1[b] += p1;
+                        } else {
+                            acc0[b] = __builtin_fmaf(p0, sc0, acc0[b]);
+                            acc1[b] = __builtin_fmaf(p1, sc1, acc1[b]);
+                        }
+                    }
+                }
+            } else {
+                // Generic: 4 columns per lane per chunk, any width/alignment.
+                const int64_t c0 = (int64_t)ch * CW + (int64_t)lane * 4;
+                if (c0 < cols) {
+                    float wv0[4], wv1[4];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const bool ok = c0 + e < cols;
+                        wv0[e] = ok ? weight_at<FMT>(w0, c0 + e) : 0.0f;
+                        wv1[e] = ok ? weight_at<FMT>(w1, c0 + e) : 0.0f;
+                    }
+                    float sc0 = 1.0f, sc1 = 1.0f;
+                    if constexpr (FMT != SRQ_F32) {
+                        sc0 = s0[c0 / kBlock];
+                        sc1 = s1[c0 / kBlock];
+                    }
+#pragma unroll
+                    for (int b = 0; b < NB; ++b) {
+                        const float4 xv = *(const float4 *)(xs + b * ld + c0);
+                        float p0 = 0.0f, p1 = 0.0f;
+                        p0 = __builtin_fmaf(xv.x, wv0[0], p0);
+                        p0 = __builtin_fmaf(xv.y, wv0[1], p0);
+                        p0 = __builtin_fmaf(xv.z, wv0[2], p0);
+                        p0 = __builtin_fmaf(xv.w, wv0[3], p0);
+                        p1 = __builtin_fmaf(xv.x, wv1[0], p1);
+                        p1 = __builtin_fmaf(xv.y, wv1[1], p1);
+                        p1 = __builtin_fmaf(xv.z, wv1[2], p1);
+                        p1 = __builtin_fmaf(xv.w, wv1[3], p1);
+                        if constexpr (FMT == SRQ_F32) {
+                            acc0[b] += p0;
+                            acc1[b] += p1;
+                        } else {
+                            acc0[b] = __builtin_fmaf(p0, sc0, acc0[b]);
+                            acc1[b] = __builtin_fmaf(p1, sc1, acc1[b]);
+                        }
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            acc0[b] = wave_sum(acc0[b]);
+            acc1[b] = wave_sum(acc1[b]);
+        }
+
+        // ---- FP64 recomputation of wide rows (cold path) -----------------
+        if (sm.any_wide) {
+#pragma unroll
+            for (int b = 0; b < NB; ++b) {
+                if (!sm.wide[b]) continue;
+                double d0 = 0.0, d1 = 0.0;
+                for (int64_t c = lane * 4; c < cols; c += 256) {
+                    double p0 = 0.0, p1 = 0.0;
+                    for (int e = 0; e < 4 && c + e < cols; ++e) {
+                        const double xv = (double)xs[b * ld + xidx<E, CW>((int)(c + e))];
+                        p0 += xv * (double)weight_at<FMT>(w0, c + e);
+                        p1 += xv * (double)weight_at<FMT>(w1, c + e);
+                    }
+                    const double sc0 = FMT == SRQ_F32 ? 1.0 : (double)s0[c / kBlock];
+                    const double sc1 = FMT == SRQ_F32 ? 1.0 : (double)s1[c / kBlock];
+                    d0 += p0 * sc0;
+                    d1 += p1 * sc1;
+                }
+                acc0[b] = (float)wave_sum_d(d0);
+                acc1[b] = (float)wave_sum_d(d1);
+            }
+        }
+
+        // ---- epilogues ---------------------------------------------------
+        if (lane == 0) {
+#pragma unroll
+            for (int b = 0; b < NB; ++b) {
+                if (b >= A.n) break;
+                float *yb = A.y + (int64_t)b * A.y_stride;
+                if constexpr (EPI == EPI_PLAIN) {
+                    yb[r0] = acc0[b];
+                    if (has1) yb[r1] = acc1[b];
+                } else if constexpr (EPI == EPI_RESID) {
+                    const float *rs = A.residual + (int64_t)b * A.y_stride;
+                    yb[r0] = rs[r0] + acc0[b];
+                    if (has1) yb[r1] = rs[r1] + acc1[b];
+                } else if constexpr (EPI == EPI_SWIGLU) {
+                    // h = f32(g / (1 + exp(-g))) * u  (M:6411-6413)
+                    const double gd = (double)acc0[b];
+                    const float sg = (float)(gd / (1.0 + exp(-gd)));
+                    yb[r0] = __fmul_rn(sg, acc1[b]);
+                } else {  // EPI_ROPE_KV
+                    float a = acc0[b], z = acc1[b];
+                    if (A.bias) {
+                        a = __fadd_rn(a, A.bias[r0]);
+                        z = __fadd_rn(z, A.bias[r1]);
+                    }
+                    const int row = A.row0 + b;
+                    const int pos = A.meta.pos[row];
+                    const int64_t qk_rows = (int64_t)A.dim + A.kvdim;
+                    if (r0 < qk_rows) {
+                        const int half = A.head_dim / 2;
+                        const int j = (int)((r0 % A.head_dim));
+                        const float c = A.cos_t[(int64_t)pos * half + j];
+                        const float s = A.sin_t[(int64_t)pos * half + j];
+                        // x' = a*c - z*s ; z' = a*s + z*c  (M:5283-5285), unfused
+                        const float na = __fsub_rn(__fmul_rn(a, c), __fmul_rn(z, s));
+                        const float nz = __fadd_rn(__fmul_rn(a, s), __fmul_rn(z, c));
+                        a = na;
+                        z = nz;
+                    }
+                    if (r0 < A.dim) {
+                        float *q = A.y + (int64_t)b * A.y_stride;
+                        q[r0] = a;
+                        q[r1] = z;
+                    } else {
+                        const int sess = A.meta.sess[row];
+                        const int page = A.meta.pages[(int64_t)sess * A.meta.pt_stride + pos / kPageTokens];
+                        float *kv = A.meta.kv_pool + (int64_t)page * A.meta.page_elems +
+                                    (int64_t)A.meta.layer * 2 * kPageTokens * A.kvdim +
+                                    (int64_t)(pos % kPageTokens) * A.kvdim;
+                        if (r0 < qk_rows) {  // K plane
+                            kv[r0 - A.dim] = a;
+                            kv[r1 - A.dim] = z;
+                        } else {  // V plane
+                            float *v = kv + (int64_t)kPageTokens * A.kvdim;
+                            v[r0 - qk_rows] = a;
+                            if (has1) v[r1 - qk_rows] = z;
+                        }
+                    }
+                }
+            }
+        }
+    }
+}
+
+template <int FMT, bool FAST, int NB, int EPI>
+int launch_t(hipStream_t s, const GemvArgs &a) {
+    using L = Lay<FMT, FAST>;
+    const int nch = (int)((a.cols + L::CW - 1) / L::CW);
+    const size_t lds = (size_t)NB * nch * L::CW * sizeof(float);
+    if (lds > 150 * 1024) return fail(SRQ_EINVAL, "gemv: activation rows do not fit LDS (n=%d cols=%lld)", NB, (long long)a.cols);
+    auto kern = gemv_kernel<FMT, FAST, NB, EPI>;
+    int64_t ngroups = EPI == EPI_SWIGLU ? a.rows / 2 : (a.rows + 1) / 2;
+    int64_t blocks = (ngroups + kWaves - 1) / kWaves;
+    // Enough waves to keep ~8 per CU busy; each wave then loops over groups.
+    const int per_cu = lds > 72 * 1024 ? 1 : lds > 48 * 1024 ? 2 : 4;
+    const int64_t cap = 256LL * per_cu * 2;
+    if (blocks > cap) blocks = cap;
+    if (blocks < 1) blocks = 1;
+    kern<<<(unsigned)blocks, kThreads, lds, s>>>(a);
+    SRQ_HIP(hipGetLastError());
+    return SRQ_OK;
+}
+
+template <int FMT, bool FAST, int EPI>
+int launch_nb(hipStream_t s, const GemvArgs &a) {
+    if (a.n <= 1) return launch_t<FMT, FAST, 1, EPI>(s, a);
+    if (a.n <= 2) return launch_t<FMT, FAST, 2, EPI>(s, a);
+    if (a.n <= 4) return launch_t<FMT, FAST, 4, EPI>(s, a);
+    return launch_t<FMT, FAST, 8, EPI>(s, a);
+}
+
+template <int FMT, bool FAST>
+int launch_epi(hipStream_t s, const GemvArgs &a) {
+    switch (a.epilogue) {
+        case EPI_PLAIN: return launch_nb<FMT, FAST, EPI_PLAIN>(s, a);
+        case EPI_RESID: return launch_nb<FMT, FAST, EPI_RESID>(s, a);
+        case EPI_SWIGLU: return launch_nb<FMT, FAST, EPI_SWIGLU>(s, a);
+        case EPI_ROPE_KV: return launch_nb<FMT, FAST, EPI_ROPE_KV>(s, a);
+    }
+    return fail(SRQ_EINVAL, "gemv: bad epilogue");
+}
+
+template <int FMT, bool FAST, int EPI>
+hipError_t prepare_nb() {
+    const void *fns[] = {(const void *)gemv_kernel<FMT, FAST, 1, EPI>, (const void *)gemv_kernel<FMT, FAST, 2, EPI>,
+                         (const void *)gemv_kernel<FMT, FAST, 4, EPI>, (const void *)gemv_kernel<FMT, FAST, 8, EPI>};
+    hipError_t err = hipSuccess;
+    for (const void *f : fns) {
+        hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, 150 * 1024);
+        if (e != hipSuccess) err = e;
+    }
+    return err;
+}
+
+template <int FMT, bool FAST>
+hipError_t prepare_epi() {
+    hipError_t e[4] = {prepare_nb<FMT, FAST, EPI_PLAIN>(), prepare_nb<FMT, FAST, EPI_RESID>(),
+                       prepare_nb<FMT, FAST, EPI_SWIGLU>(), prepare_nb<FMT, FAST, EPI_ROPE_KV>()};
+    for (hipError_t x : e)
+        if (x != hipSuccess) return x;
+    return hipSuccess;
+}
+
+}  // namespace
+
+// Raise the dynamic LDS limit of every GEMV instantiation once per device,
+// before any launch (also before graph capture).
+int gemv_prepare() {
+    const hipError_t errs[] = {prepare_epi<SRQ_Q8, true>(),  prepare_epi<SRQ_Q8, false>(),
+                               prepare_epi<SRQ_Q4, true>(),  prepare_epi<SRQ_Q4, false>(),
+                               prepare_epi<SRQ_F32, true>(), prepare_epi<SRQ_F32, false>()};
+    for (hipError_t e : errs)
+        if (e != hipSuccess) return fail(SRQ_EDEVICE, "gemv LDS attribute: %s", hipGetErrorString(e));
+    return SRQ_OK;
+}
+
+// Largest batch (8, 4, 2 or 1) whose staged activations fit the LDS budget,
+// or 0 when even one row does not fit.
+int gemv_max_rows(int fmt, int64_t cols) {
+    const bool fast = gemv_fast_ok(fmt, cols);
+    const int64_t cw = !fast ? 256 : fmt == SRQ_Q8 ? 1024 : fmt == SRQ_Q4 ? 2048 : 256;
+    const int64_t ld = (cols + cw - 1) / cw * cw;
+    for (int nb = 8; nb >= 1; nb /= 2)
+        if (nb * ld * 4 <= 150 * 1024) return nb;
+    return 0;
+}
+
+bool gemv_fast_ok(int fmt, int64_t cols) {
+    if (fmt == SRQ_Q8) return cols % 16 == 0;
+    if (fmt == SRQ_Q4) return cols % 32 == 0;
+    return cols % 4 == 0;
+}
+
+int launch_gemv(hipStream_t s, const GemvArgs &a) {
+    if (a.n < 1 || a.n > 8) return fail(SRQ_EINVAL, "gemv: n=%d outside 1..8", a.n);
+    if (a.rows <= 0 || a.cols <= 0) return SRQ_OK;
+    const bool fast = gemv_fast_ok(a.fmt, a.cols) && ((uintptr_t)a.values & 15) == 0;
+    switch (a.fmt) {
+        case SRQ_Q8: return fast ? launch_epi<SRQ_Q8, true>(s, a) : launch_epi<SRQ_Q8, false>(s, a);
+        case SRQ_Q4: return fast ? launch_epi<SRQ_Q4, true>(s, a) : launch_epi<SRQ_Q4, false>(s, a);
+        case SRQ_F32: return fast ? launch_epi<SRQ_F32, true>(s, a) : launch_epi<SRQ_F32, false>(s, a);
+    }
+    return fail(SRQ_EINVAL, "gemv: bad format");
+}
+
+}  // namespace srq

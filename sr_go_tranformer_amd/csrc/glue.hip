@@ -1,0 +1,198 @@
+// Step glue kernels used on the batched (GEMM) path and around it.
+// cmd/monolith/monolith.go: rmsInto M:6182-6194, rope M:5264-5289, KV row
+// write M:6393-6395, SwiGLU M:6411-6413, selective-head compaction and
+// expansion M:6420-6448, greedy argmax M:1215-1223.
+#include "srq_internal.h"
+
+namespace srq {
+namespace {
+
+__device__ __forceinline__ double block_sum_d(double v, double *red) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    double t = 0.0;
+    for (int w = 0; w < (int)(blockDim.x >> 6); ++w) t += red[w];
+    __syncthreads();
+    return t;
+}
+
+// rmsInto: a = f32(1/sqrt(sum f64(x^2)/d + eps)); y = (x*a)*w.
+__global__ __launch_bounds__(256) void rmsnorm_kernel(const float *__restrict__ x, const float *__restrict__ w,
+                                                      float *__restrict__ y, int32_t d, double eps) {
+    __shared__ double red[4];
+    const float *xr = x + (int64_t)blockIdx.x * d;
+    float *yr = y + (int64_t)blockIdx.x * d;
+    double ss = 0.0;
+    for (int j = threadIdx.x; j < d; j += 256) ss += (double)xr[j] * (double)xr[j];
+    ss = block_sum_d(ss, red);
+    const float a = (float)(1.0 / sqrt(ss / (double)d + eps));
+    for (int j = threadIdx.x; j < d; j += 256) yr[j] = __fmul_rn(__fmul_rn(xr[j], a), w[j]);
+}
+
+// qkv row [q: dim | k: kvdim | v: kvdim] (+bias) -> q_out (roped), K (roped)
+// and V into the row's KV page.
+__global__ __launch_bounds__(256) void rope_kv_kernel(const float *__restrict__ qkv, const float *__restrict__ bias,
+                                                      int32_t dim, int32_t kvdim, int32_t head_dim,
+                                                      const float *__restrict__ cos_t,
+                                                      const float *__restrict__ sin_t, float *__restrict__ q_out,
+                                                      const RowMeta meta) {
+    const int row = blockIdx.x;
+    const int width = dim + 2 * kvdim;
+    const float *src = qkv + (int64_t)row * width;
+    const int pos = meta.pos[row];
+    const int half = head_dim / 2;
+    const int page = meta.pages[(int64_t)meta.sess[row] * meta.pt_stride + pos / kPageTokens];
+    float *kr = meta.kv_pool + (int64_t)page * meta.page_elems + (int64_t)meta.layer * 2 * kPageTokens * kvdim +
+                (int64_t)(pos % kPageTokens) * kvdim;
+    float *vr = kr + (int64_t)kPageTokens * kvdim;
+    const int pairs = (dim + kvdim) / 2;
+    for (int p = threadIdx.x; p < pairs; p += 256) {
+        const int h = p / half, j = p - h * half;
+        const int i0 = h * head_dim + j, i1 = i0 + half;
+        float a = src[i0], z = src[i1];
+        if (bias) {
+            a = __fadd_rn(a, bias[i0]);
+            z = __fadd_rn(z, bias[i1]);
+        }
+        const float c = cos_t[(int64_t)pos * half + j], s = sin_t[(int64_t)pos * half + j];
+        const float na = __fsub_rn(__fmul_rn(a, c), __fmul_rn(z, s));
+        const float nz = __fadd_rn(__fmul_rn(a, s), __fmul_rn(z, c));
+        if (i0 < dim) {
+            q_out[(int64_t)row * dim + i0] = na;
+            q_out[(int64_t)row * dim + i1] = nz;
+        } else {
+            kr[i0 - dim] = na;
+            kr[i1 - dim] = nz;
+        }
+    }
+    for (int j = threadIdx.x; j < kvdim; j += 256) {
+        float v = src[dim + kvdim + j];
+        if (bias) v = __fadd_rn(v, bias[dim + kvdim + j]);
+        vr[j] = v;
+    }
+}
+
+// gu row [gate: hidden | up: hidden] -> h = f32(g/(1+exp(-g))) * u.
+__global__ __launch_bounds__(256) void swiglu_kernel(const float *__restrict__ gu, int32_t hidden,
+                                                     float *__restrict__ h) {
+    const float *src = gu + (int64_t)blockIdx.y * 2 * hidden;
+    float *dst = h + (int64_t)blockIdx.y * hidden;
+    for (int j = blockIdx.x * 256 + threadIdx.x; j < hidden; j += gridDim.x * 256) {
+        const double g = (double)src[j];
+        const float sg = (float)(g / (1.0 + exp(-g)));
+        dst[j] = __fmul_rn(sg, src[hidden + j]);
+    }
+}
+
+// dst[i] = src[rows[i]] (rows[i] < 0: zero row).
+__global__ __launch_bounds__(256) void gather_kernel(const float *__restrict__ src, int64_t d,
+                                                     const int32_t *__restrict__ rows, float *__restrict__ dst) {
+    const int32_t r = rows[blockIdx.y];
+    float *out = dst + (int64_t)blockIdx.y * d;
+    for (int64_t j = (int64_t)blockIdx.x * 256 + threadIdx.x; j < d; j += (int64_t)gridDim.x * 256)
+        out[j] = r >= 0 ? src[(int64_t)r * d + j] : 0.0f;
+}
+
+// First maximum with strict '>' (lowest id wins ties); non-finite -> err.
+__global__ __launch_bounds__(256) void argmax_kernel(const float *__restrict__ logits, int32_t vocab,
+                                                     int32_t *__restrict__ ids, int32_t *__restrict__ err) {
+    __shared__ float bv[4];
+    __shared__ int bi[4];
+    __shared__ int bad;
+    if (threadIdx.x == 0) bad = 0;
+    __syncthreads();
+    const float *row = logits + (int64_t)blockIdx.x * vocab;
+    float best = 0.0f;
+    int idx = -1;
+    int nonfinite = 0;
+    for (int j = threadIdx.x; j < vocab; j += 256) {
+        const float v = row[j];
+        if (!isfinite(v)) nonfinite = 1;
+        if (idx < 0 || v > best) best = v, idx = j;  // ascending j per thread
+    }
+    if (nonfinite) bad = 1;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(best, o, 64);
+        const int oi = __shfl_xor(idx, o, 64);
+        if (oi >= 0 && (idx < 0 || ov > best || (ov == best && oi < idx))) best = ov, idx = oi;
+    }
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (lane == 0) bv[wave] = best, bi[wave] = idx;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float b = bv[0];
+        int i = bi[0];
+        for (int w = 1; w < 4; ++w)
+            if (bi[w] >= 0 && (i < 0 || bv[w] > b || (bv[w] == b && bi[w] < i))) b = bv[w], i = bi[w];
+        ids[blockIdx.x] = i;
+        if (bad) err[0] = 1;
+    }
+}
+
+// One decode step of a replayed greedy loop: record the token, feed it to
+// the next embedding lookup and advance the position.
+__global__ void advance_kernel(int32_t *pos, const int32_t *token, int32_t *out, int32_t *counter,
+                               int32_t *embed_ids) {
+    if (threadIdx.x == 0 && blockIdx.x == 0) {
+        const int t = token[0];
+        out[counter[0]] = t;
+        counter[0] = counter[0] + 1;
+        embed_ids[0] = t;
+        pos[0] = pos[0] + 1;
+    }
+}
+
+}  // namespace
+
+int launch_rmsnorm(hipStream_t s, const float *x, const float *w, float *y, int32_t n, int32_t d, double eps) {
+    if (n <= 0) return SRQ_OK;
+    rmsnorm_kernel<<<n, 256, 0, s>>>(x, w, y, d, eps);
+    SRQ_HIP(hipGetLastError());
+    return SRQ_OK;
+}
+
+int launch_rope_kv(hipStream_t s, const float *qkv, const float *bias, int32_t n, int32_t dim, int32_t kvdim,
+                   int32_t head_dim, const float *cos_t, const float *sin_t, float *q_out, const RowMeta &meta) {
+    if (n <= 0) return SRQ_OK;
+    rope_kv_kernel<<<n, 256, 0, s>>>(qkv, bias, dim, kvdim, head_dim, cos_t, sin_t, q_out, meta);
+    SRQ_HIP(hipGetLastError());
+    return SRQ_OK;
+}
+
+int launch_swiglu(hipStream_t s, const float *gu, int32_t n, int32_t hidden, float *h) {
+    if (n <= 0) return SRQ_OK;
+    int bx = (hidden + 255) / 256;
+    if (bx > 64) bx = 64;
+    swiglu_kernel<<<dim3(bx, n), 256, 0, s>>>(gu, hidden, h);
+    SRQ_HIP(hipGetLastError());
+    return SRQ_OK;
+}
+
+int launch_gather_rows(hipStream_t s, const float *src, int64_t d, const int32_t *rows, int32_t count, float *dst) {
+    if (count <= 0) return SRQ_OK;
+    int64_t bx = (d + 255) / 256;
+    if (bx > 64) bx = 64;
+    gather_kernel<<<dim3((unsigned)bx, count), 256, 0, s>>>(src, d, rows, dst);
+    SRQ_HIP(hipGetLastError());
+    return SRQ_OK;
+}
+
+int launch_argmax(hipStream_t s, const float *logits, int32_t rows, int32_t vocab, int32_t *ids, int32_t *err) {
+    if (rows <= 0) return SRQ_OK;
+    argmax_kernel<<<rows, 256, 0, s>>>(logits, vocab, ids, err);
+    SRQ_HIP(hipGetLastError());
+    return SRQ_OK;
+}
+
+int launch_advance(hipStream_t s, int32_t *pos, const int32_t *token, int32_t *out, int32_t *counter,
+                   int32_t *embed_ids) {
+    advance_kernel<<<1, 64, 0, s>>>(pos, token, out, counter, embed_ids);
+    SRQ_HIP(hipGetLastError());
+    return SRQ_OK;
+}
+
+}  // namespace srq

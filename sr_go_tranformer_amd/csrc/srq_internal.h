@@ -1,0 +1,141 @@
+// Internal declarations shared by the gfx950 kernels and the C-ABI runtime.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/srq.h"
+
+namespace srq {
+
+constexpr int kBlock = 64;       // q8Block (M:3793): scale block width
+constexpr int kPageTokens = 32;  // pageTokens (M:5846)
+constexpr int kWave = 64;
+
+// f32(MaxFloat32 / (2*64*127)) (M:4346-4354): above it a row takes the
+// FP64 path.  The constant is the correctly rounded f32 of the quotient.
+constexpr float kWideLimit = 0x1.020408p+114f;  // 2.0932724e34
+
+// Streaming (read-once) loads of packed weights: global_load ... nt.
+typedef uint32_t srq_u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t srq_u32x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint4 ld_stream16(const void *p) {
+    const srq_u32x4 v = __builtin_nontemporal_load((const srq_u32x4 *)p);
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint2 ld_stream8(const void *p) {
+    const srq_u32x2 v = __builtin_nontemporal_load((const srq_u32x2 *)p);
+    return make_uint2(v.x, v.y);
+}
+
+// Error reporting: sets the calling thread's message and returns code.
+int fail(int code, const char *fmt, ...);
+void clear_error();
+
+#define SRQ_HIP(expr)                                                                          \
+    do {                                                                                       \
+        hipError_t _e = (expr);                                                                \
+        if (_e != hipSuccess) return ::srq::fail(SRQ_EDEVICE, "%s: %s", #expr, hipGetErrorString(_e)); \
+    } while (0)
+
+#define SRQ_CHECK(expr)           \
+    do {                          \
+        int _rc = (expr);         \
+        if (_rc != SRQ_OK) return _rc; \
+    } while (0)
+
+// Byte stride of one packed row.
+__host__ __device__ inline int64_t row_bytes(int fmt, int64_t cols) {
+    return fmt == SRQ_Q8 ? cols : fmt == SRQ_Q4 ? (cols + 1) / 2 : cols * 4;
+}
+__host__ __device__ inline int64_t groups_of(int64_t cols) { return (cols + kBlock - 1) / kBlock; }
+
+// ---------------------------------------------------------------- packing
+int launch_pack(hipStream_t s, int fmt, int64_t rows, int64_t cols, const void *src, int dtype, void *values,
+                float *scales, int *err_flag);
+int launch_convert_f32(hipStream_t s, int64_t count, const void *src, int dtype, float *dst, int *err_flag);
+int launch_dequant_rows(hipStream_t s, int fmt, int64_t cols, const void *values, const float *scales,
+                        const int32_t *rows, int32_t count, float *dst);
+
+// ------------------------------------------------------------------ GEMV
+enum Epilogue { EPI_PLAIN = 0, EPI_RESID = 1, EPI_SWIGLU = 2, EPI_ROPE_KV = 3 };
+
+// Row metadata of a step: per activation row its position and session,
+// per session a page table of pt_stride int32 page ids.
+struct RowMeta {
+    const int32_t *pos;        // [n]
+    const int32_t *sess;       // [n]
+    const int32_t *pages;      // [sessions x pt_stride]
+    int32_t pt_stride;
+    float *kv_pool;            // page 0
+    int64_t page_elems;        // 2*32*kvdim*layers
+    int32_t layer;
+};
+
+struct GemvArgs {
+    int fmt;
+    const void *values;
+    const float *scales;
+    int64_t rows, cols;        // W is [rows x cols]
+    const float *x;            // [n x cols]
+    int32_t n;                 // activation rows (1..8 per launch)
+    int32_t row0;              // index of x's first row in the step (RowMeta)
+    const float *norm_w;       // fused RMSNorm weight [cols] or null
+    double norm_eps;
+    float *y;                  // output
+    int64_t y_stride;
+    int epilogue;
+    const float *residual;     // EPI_RESID: y = residual + dot (may alias y)
+    // EPI_ROPE_KV: W rows are [q: dim | k: kvdim | v: kvdim]
+    int32_t dim, kvdim, head_dim;
+    const float *cos_t, *sin_t; // [context x head_dim/2]
+    const float *bias;          // [rows] or null, added before RoPE
+    RowMeta meta;
+};
+int launch_gemv(hipStream_t s, const GemvArgs &a);
+bool gemv_fast_ok(int fmt, int64_t cols);
+int gemv_max_rows(int fmt, int64_t cols);
+int gemv_prepare();
+
+// ------------------------------------------------------------------ GEMM
+struct GemmArgs {
+    int fmt;
+    const void *values;
+    const float *scales;
+    int64_t rows, cols;
+    const float *x;     // [n x cols]
+    int32_t n;
+    float *y;           // [n x y_stride]
+    int64_t y_stride;
+    const float *residual;  // y = residual + acc when non-null (may alias y)
+};
+// wide: per-row flags from launch_wide_scan (rows set are left to wide_fix).
+int launch_gemm(hipStream_t s, const GemmArgs &a, const int32_t *wide);
+bool gemm_ok(int fmt, int64_t cols);
+// Per-row wide flags of x [n x cols] (1 if any |x| > kWideLimit) and the
+// FP64 recomputation of flagged rows.
+int launch_wide_scan(hipStream_t s, const float *x, int32_t n, int64_t cols, int32_t *flags);
+int launch_wide_fix(hipStream_t s, const GemmArgs &a, const int32_t *flags);
+
+// ------------------------------------------------------------------ glue
+int launch_rmsnorm(hipStream_t s, const float *x, const float *w, float *y, int32_t n, int32_t d, double eps);
+int launch_rope_kv(hipStream_t s, const float *qkv, const float *bias, int32_t n, int32_t dim, int32_t kvdim,
+                   int32_t head_dim, const float *cos_t, const float *sin_t, float *q_out, const RowMeta &meta);
+int launch_swiglu(hipStream_t s, const float *gu, int32_t n, int32_t hidden, float *h);
+int launch_gather_rows(hipStream_t s, const float *src, int64_t d, const int32_t *rows, int32_t count, float *dst);
+int launch_argmax(hipStream_t s, const float *logits, int32_t rows, int32_t vocab, int32_t *ids, int32_t *err);
+int launch_advance(hipStream_t s, int32_t *pos, const int32_t *token, int32_t *out, int32_t *counter,
+                   int32_t *embed_ids);
+
+// ------------------------------------------------------------- attention
+struct AttnArgs {
+    const float *q;     // [n x heads*head_dim]
+    float *out;         // [n x heads*head_dim]
+    int32_t n, heads, kv_heads, head_dim;
+    int32_t max_len;    // upper bound of pos+1 over rows (sizes LDS)
+    RowMeta meta;
+};
+int launch_attention(hipStream_t s, const AttnArgs &a);
+int attention_prepare();
+
+}  // namespace srq
