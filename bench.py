@@ -1,0 +1,277 @@
+#!/usr/bin/env python3
+"""Q8 decode benchmark on one MI355X: Mistral-7B shape, batch 1.
+
+Workload (the configuration the headline metric is quoted on): a
+Mistral-7B-shape decoder (hidden 4096, 32 layers, 32 query / 8 KV heads,
+SwiGLU 14336, vocab 32768, untied head) with seeded N(0, 0.02) weights
+packed to Q8 on the device, a 128-token uniform-random prompt prefilled in
+one chunk, then greedy decode (graph-replayed steps, device argmax) with
+32-token KV pages.  One step = one decode token.  --warmup W steps run
+untimed, then exactly --steps K steps are timed with HIP events on the
+executor's stream (bracketed by stream synchronisation).
+
+Reported:
+  value          weight bytes streamed per decode token x tokens/s (GB/s)
+  roofline       the Q8 dequant-GEMV kernel at 14336 x 4096, batch 1,
+                 timed launch by launch with HIP events over the 32 distinct
+                 up-projection matrices (2 GB, far beyond the 256 MB MALL)
+  cpu_baseline   the oracle (C restatement of the reference's Go CPU path)
+                 decoding a few tokens of the same model on the host cores
+"""
+import argparse
+import ctypes as C
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+PROMPT, TOKENS = 128, 256
+# Reference receipt for the same workload: Mistral-7B Q8 decode, batch 1,
+# Apple M4, GOMAXPROCS=4: 0.750 s/token = 1.33 tok/s = 10.1 GB/s of weights.
+REF_GBS = 10.1
+
+
+class HipEvents:
+    """hipEventCreate/Record/ElapsedTime on an explicit stream."""
+
+    def __init__(self):
+        self.hip = C.CDLL("libamdhip64.so")
+        self.hip.hipEventCreate.argtypes = [C.POINTER(C.c_void_p)]
+        self.hip.hipEventRecord.argtypes = [C.c_void_p, C.c_void_p]
+        self.hip.hipEventSynchronize.argtypes = [C.c_void_p]
+        self.hip.hipEventElapsedTime.argtypes = [C.POINTER(C.c_float), C.c_void_p, C.c_void_p]
+        self.hip.hipEventDestroy.argtypes = [C.c_void_p]
+
+    def create(self):
+        e = C.c_void_p()
+        assert self.hip.hipEventCreate(C.byref(e)) == 0
+        return e
+
+    def record(self, ev, stream):
+        assert self.hip.hipEventRecord(ev, stream) == 0
+
+    def elapsed_ms(self, a, b):
+        assert self.hip.hipEventSynchronize(b) == 0
+        ms = C.c_float()
+        assert self.hip.hipEventElapsedTime(C.byref(ms), a, b) == 0
+        return ms.value
+
+    def destroy(self, ev):
+        self.hip.hipEventDestroy(ev)
+
+
+def gemv_roofline(srq, ex, model, cfg, hip, launches):
+    """Time the Q8 GEMV at 14336x4096 (batch 1) launch by launch."""
+    ups = [model.weight(srq.T_UP, layer) for layer in range(cfg.layers)]
+    rows, cols = ups[0].rows, ups[0].cols
+    x = ex.empty(cols * 4)
+    srq.fill_normal(ex, x, cols, 7, 1.0)
+    y = ex.empty(rows * 4)
+    stream = C.c_void_p(ex.stream)
+    L = srq.lib()
+    for w in ups[:4]:  # warm the code path
+        srq.check(L.srq_linear_enqueue(ex.h, y.ptr, x.ptr, w.h, 1))
+    ex.synchronize()
+    evs = [(hip.create(), hip.create()) for _ in range(launches)]
+    for i, (a, b) in enumerate(evs):
+        hip.record(a, stream)
+        srq.check(L.srq_linear_enqueue(ex.h, y.ptr, x.ptr, ups[i % len(ups)].h, 1))
+        hip.record(b, stream)
+    ex.synchronize()
+    ms = [hip.elapsed_ms(a, b) for a, b in evs]
+    for a, b in evs:
+        hip.destroy(a)
+        hip.destroy(b)
+    vb, sb = srq.packed_bytes(srq.Q8, rows, cols)
+    algo = vb + sb + cols * 4 + rows * 4
+    avg_s = float(np.mean(ms)) / 1e3
+    achieved = algo / avg_s / 1e9
+    return {
+        "kernel": "gemv_stream_kernel<Q8, n=1, plain> 14336x4096",
+        "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+        "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": read_traffic(),
+        "algorithmic_bytes_per_launch": algo, "avg_launch_us": round(avg_s * 1e6, 3),
+        "launches": launches,
+    }
+
+
+def read_traffic():
+    """HBM bytes per launch from the committed rocprofv3 --pmc summary."""
+    path = os.path.join(ROOT, "profiles", "gemv_q8_14336x4096_pmc.txt")
+    try:
+        for line in open(path):
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(float(line.split(":")[1]))
+    except OSError:
+        pass
+    return None
+
+
+def cpu_baseline(srq, ex, model, cfg, cache, first, gpu_tokens, n_tokens):
+    """Decode n_tokens of the same model with the oracle on the host."""
+    import oracle
+    t_setup = time.perf_counter()
+    weights = {}
+
+    def take(name, w):
+        vals, scl = w.packed(ex)
+        weights[name] = oracle.Weight(oracle.Q8, w.rows, w.cols, vals.view(np.int8).reshape(w.rows, w.cols),
+                                      scl.reshape(w.rows, -1))
+
+    take("embed_tokens", model.weight(srq.T_EMBED))
+    take("lm_head", model.weight(srq.T_OUTPUT))
+    names = {"q_proj": srq.T_Q, "k_proj": srq.T_K, "v_proj": srq.T_V, "o_proj": srq.T_O, "gate_proj": srq.T_GATE,
+             "up_proj": srq.T_UP, "down_proj": srq.T_DOWN}
+    ones = np.ones(cfg.dim, np.float32)
+    for layer in range(cfg.layers):
+        for nm, kind in names.items():
+            take("layers.%d.%s" % (layer, nm), model.weight(kind, layer))
+        for nm in ("input_layernorm", "post_attention_layernorm"):
+            weights["layers.%d.%s" % (layer, nm)] = oracle.Weight(oracle.F32, 1, cfg.dim, ones)
+    weights["norm"] = oracle.Weight(oracle.F32, 1, cfg.dim, ones)
+    ocfg = oracle.make_config(cfg.vocab, cfg.dim, cfg.layers, cfg.heads, cfg.kv_heads, cfg.hidden, cfg.context,
+                              cfg.rope_theta, cfg.norm_eps, False)
+    om = oracle.Model(ocfg, weights)
+    oc = om.new_cache()
+    for layer in range(cfg.layers):
+        k, v = cache.read(layer, 0, PROMPT)
+        oc.set_rows(layer, 0, k, v)
+    oc.set_pos(PROMPT)
+    setup_s = time.perf_counter() - t_setup
+    workers = min(os.cpu_count() or 1, 16)
+    feed = [first] + gpu_tokens
+    t0 = time.perf_counter()
+    produced = []
+    for i in range(n_tokens):
+        logits = om.step([oc], [[feed[i]]], workers=workers)[0]
+        produced.append(oracle.argmax(logits))
+    dt = time.perf_counter() - t0
+    tps = n_tokens / dt
+    om.close()
+    return tps, workers, produced, setup_s
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=240, help="timed decode tokens")
+    ap.add_argument("--warmup", type=int, default=15, help="untimed decode tokens")
+    ap.add_argument("--seed", type=int, default=1)
+    ap.add_argument("--cpu-tokens", type=int, default=6, help="decode tokens of the CPU baseline sample")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--gemv-launches", type=int, default=320)
+    ap.add_argument("--eager", action="store_true",
+                    help="launch each decode kernel directly instead of replaying the captured graph "
+                         "(for kernel tracers that cannot follow graph launches)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (--gpus must be 1).", file=sys.stderr)
+        return 2
+    if args.steps < 1 or args.warmup < 0 or args.steps + args.warmup > TOKENS - 1:
+        print("need 1 <= steps and steps + warmup <= %d (a %d-token generation)" % (TOKENS - 1, TOKENS),
+              file=sys.stderr)
+        return 2
+
+    import sr_go_tranformer_amd as srq
+    from sr_go_tranformer_amd import synthetic
+
+    t_start = time.perf_counter()
+    ex = srq.Executor(0)
+    cfg = synthetic.shape_config("mistral-7b", PROMPT + TOKENS)
+    model = synthetic.build(ex, cfg, "q8", args.seed)
+    build_s = time.perf_counter() - t_start
+    resident = model.resident_bytes()
+    print("model built in %.1f s, resident %d bytes" % (build_s, resident), file=sys.stderr, flush=True)
+
+    hip = HipEvents()
+    stream = C.c_void_p(ex.stream)
+    pool = model.pool(16)
+    cache = pool.cache((PROMPT + TOKENS + 31) // 32)
+    prompt = synthetic.random_prompt(PROMPT, cfg.vocab, args.seed)
+    ex.synchronize()
+    t0 = time.perf_counter()
+    model.step([cache], [prompt])
+    prefill_s = time.perf_counter() - t0
+    first = int(model.argmax_last()[0])
+
+    dec = srq.Decoder(model, cache, first, args.warmup + args.steps, eager=args.eager)
+    dec.run(args.warmup)
+    ex.synchronize()
+    ev0, ev1 = hip.create(), hip.create()
+    hip.record(ev0, stream)
+    dec.run(args.steps)
+    hip.record(ev1, stream)
+    ex.synchronize()
+    decode_ms = hip.elapsed_ms(ev0, ev1)
+    tokens = dec.tokens()
+    dec.close()
+    print("decode %d tokens in %.2f ms" % (args.steps, decode_ms), file=sys.stderr, flush=True)
+
+    ms_per_step = decode_ms / args.steps
+    tok_s = 1e3 / ms_per_step
+    wbytes = synthetic.decode_weight_bytes(cfg, "q8")
+    gbs = wbytes * tok_s / 1e9
+    kd = cfg.dim // cfg.heads * cfg.kv_heads
+    pos_mid = PROMPT + args.warmup + args.steps / 2.0
+    kv_bytes = 2 * pos_mid * kd * 4 * cfg.layers
+
+    roof = gemv_roofline(srq, ex, model, cfg, hip, args.gemv_launches)
+    print("gemv %.1f GB/s" % roof["achieved"], file=sys.stderr, flush=True)
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        n = max(1, args.cpu_tokens)
+        tps, workers, produced, setup_s = cpu_baseline(srq, ex, model, cfg, cache, first, tokens, n)
+        cpu = {"value": round(wbytes * tps / 1e9, 3), "unit": "GB/s", "tokens_per_s": round(tps, 4),
+               "cores": workers, "kind": "port",
+               "sample": "%d greedy decode tokens of the same Mistral-7B-shape Q8 model from position %d "
+                         "(KV rows copied from the GPU prefill), oracle C restatement of the reference Go "
+                         "CPU path, %d worker threads (GOMAXPROCS-equivalent), %s" %
+                         (n, PROMPT, workers, os.uname().machine),
+               "greedy_match": produced == tokens[:n] if n <= len(tokens) else None}
+        print("cpu %.3f tok/s" % tps, file=sys.stderr, flush=True)
+
+    out = {
+        "metric": "Q8 decode GEMV HBM GB/s (% of peak) + tokens/s, 7B-shape, batch 1",
+        "value": round(gbs, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": round(gbs / REF_GBS, 1),
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {
+            "workload": "Mistral-7B-shape Q8 greedy decode, batch 1, 128-token random prompt, 256 tokens",
+            "hidden": cfg.dim, "layers": cfg.layers, "heads": cfg.heads, "kv_heads": cfg.kv_heads,
+            "intermediate": cfg.hidden, "vocab": cfg.vocab, "page_tokens": 32, "weights": "int8 Q8, f32 scales/64",
+            "prompt_tokens": PROMPT, "generated_tokens": TOKENS, "seed": args.seed,
+            "decode_launch": "eager" if args.eager else "hip-graph",
+            "vs_baseline_reference": "Mistral-7B Q8 decode batch 1 on Apple M4 (GOMAXPROCS=4): 1.33 tok/s, "
+                                     "10.1 GB/s of weights",
+        },
+        "tokens_per_s": round(tok_s, 2),
+        "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
+        "weight_bytes_per_token": wbytes,
+        "kv_bytes_per_token_mid": int(kv_bytes),
+        "prefill_tokens_per_s": round(PROMPT / prefill_s, 1),
+        "resident_weight_bytes": resident,
+        "roofline": roof,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -86,6 +86,14 @@ int srq_packed_bytes(srq_format fmt, int64_t rows, int64_t cols, int64_t *values
 int srq_pack(srq_exec *e, srq_format fmt, int64_t rows, int64_t cols, const void *src, srq_src_dtype dtype,
              void *values, float *scales);
 
+/* Synthetic initialisation: dst[i] = f32(Normal()*scale) of the reference's
+ * RNG seeded with `seed` (RNG{seed}.Normal, M:1411-1439, as NewModel draws
+ * weights, M:5218): element i uses the SplitMix64 draws 2i+1 and 2i+2, so
+ * the device fills in parallel the sequence a serial RNG would produce
+ * (FP64 log/cos may differ from Go's in the last ulp before the f32
+ * rounding).  dst is device memory. */
+int srq_fill_normal(srq_exec *e, float *dst, int64_t count, uint64_t seed, double scale);
+
 /* ---- weights: Param{Rows, Cols, Q8, Q4, Data} (M:3784-3791) ------------ */
 /* Allocate device storage and pack (Q8/Q4) or convert (F32) from src. */
 int srq_weight_create(srq_exec *e, srq_format fmt, int64_t rows, int64_t cols, const void *src,
@@ -107,6 +115,10 @@ int srq_dequant_rows(srq_exec *e, const srq_weight *w, const int32_t *rows, int3
  * batch; for n <= 16 they are also bit-identical to the row computed
  * alone. */
 int srq_linear(srq_exec *e, float *y, const float *x, const srq_weight *w, int32_t n);
+/* Same computation, stream-ordered on the executor without joining: for
+ * callers that chain work on the executor's stream (or time it with HIP
+ * events).  Inputs must stay valid until the stream reaches the call. */
+int srq_linear_enqueue(srq_exec *e, float *y, const float *x, const srq_weight *w, int32_t n);
 
 /* ---- model: HF Llama/Mistral/Qwen2 profile (M:4985-5050) --------------- */
 typedef struct {
@@ -194,8 +206,12 @@ int srq_argmax(srq_exec *e, const float *logits, int32_t rows, int32_t vocab, in
  * The decoder owns its workspace; the cache must not be stepped elsewhere
  * while a decoder on it is alive. */
 typedef struct srq_decoder srq_decoder;
+/* flags: SRQ_DECODER_EAGER launches every kernel of each step directly
+ * instead of replaying a captured graph (for tracers that cannot follow
+ * graph launches); results are identical. */
+#define SRQ_DECODER_EAGER 1
 int srq_decoder_create(srq_exec *e, srq_model *m, srq_cache *c, int32_t first_token, int32_t max_steps,
-                       srq_decoder **out);
+                       int32_t flags, srq_decoder **out);
 int srq_decoder_run(srq_decoder *d, int32_t steps);
 int srq_decoder_tokens(srq_decoder *d, int32_t *out, int32_t *count);
 int srq_decoder_destroy(srq_decoder *d);

@@ -350,13 +350,13 @@ def rms(x, w, eps):
     return y
 
 
-def greedy(model, ids, count, chunk):
+def greedy(model, ids, count, chunk, workers=8):
     """inferHFIDs (M:1185-1240) without EOS stop: prefill in chunks, then
     count greedy tokens (fixed-step).  Returns (tokens, last-step logits list)."""
     cache = model.new_cache()
     nxt = None
     for lo in range(0, len(ids), chunk):
-        nxt = model.step([cache], [ids[lo:lo + chunk]])[0]
+        nxt = model.step([cache], [ids[lo:lo + chunk]], workers=workers)[0]
     out, logits = [], []
     for i in range(count):
         best = argmax(nxt)
@@ -365,6 +365,6 @@ def greedy(model, ids, count, chunk):
         logits.append(nxt)
         out.append(best)
         if i + 1 < count:
-            nxt = model.step([cache], [[best]])[0]
+            nxt = model.step([cache], [[best]], workers=workers)[0]
     cache.close()
     return out, logits

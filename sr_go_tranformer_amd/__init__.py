@@ -58,8 +58,8 @@ def lib():
 EXPORTS = [
     "srq_abi_version", "srq_last_error", "srq_device_count", "srq_alloc", "srq_free", "srq_copy_h2d",
     "srq_copy_d2h", "srq_copy_d2d", "srq_exec_create", "srq_exec_destroy", "srq_exec_synchronize",
-    "srq_exec_stream", "srq_packed_bytes", "srq_pack", "srq_weight_create", "srq_weight_wrap",
-    "srq_weight_destroy", "srq_weight_info", "srq_dequant_rows", "srq_linear", "srq_model_create",
+    "srq_exec_stream", "srq_fill_normal", "srq_packed_bytes", "srq_pack", "srq_weight_create", "srq_weight_wrap",
+    "srq_weight_destroy", "srq_weight_info", "srq_dequant_rows", "srq_linear", "srq_linear_enqueue", "srq_model_create",
     "srq_model_load", "srq_model_destroy", "srq_model_resident_bytes", "srq_model_weight",
     "srq_model_rope_tables", "srq_pool_create", "srq_pool_destroy", "srq_cache_create", "srq_cache_destroy",
     "srq_cache_pos", "srq_cache_read", "srq_step", "srq_argmax", "srq_decoder_create", "srq_decoder_run",
@@ -83,6 +83,7 @@ def _declare(L):
         "srq_exec_destroy": (C.c_int, [P]),
         "srq_exec_synchronize": (C.c_int, [P]),
         "srq_exec_stream": (P, [P]),
+        "srq_fill_normal": (C.c_int, [P, P, I64, C.c_uint64, C.c_double]),
         "srq_packed_bytes": (C.c_int, [C.c_int, I64, I64, C.POINTER(I64), C.POINTER(I64)]),
         "srq_pack": (C.c_int, [P, C.c_int, I64, I64, P, C.c_int, P, P]),
         "srq_weight_create": (C.c_int, [P, C.c_int, I64, I64, P, C.c_int, PP]),
@@ -91,6 +92,7 @@ def _declare(L):
         "srq_weight_info": (C.c_int, [P, C.POINTER(C.c_int), C.POINTER(I64), C.POINTER(I64), PP, PP]),
         "srq_dequant_rows": (C.c_int, [P, P, P, I32, P]),
         "srq_linear": (C.c_int, [P, P, P, P, I32]),
+        "srq_linear_enqueue": (C.c_int, [P, P, P, P, I32]),
         "srq_model_create": (C.c_int, [P, C.POINTER(ModelConfig), C.c_char_p, PP]),
         "srq_model_load": (C.c_int, [P, C.c_int, C.c_int, P, C.c_int]),
         "srq_model_destroy": (C.c_int, [P]),
@@ -105,7 +107,7 @@ def _declare(L):
         "srq_cache_read": (C.c_int, [P, P, I32, I32, I32, P, P]),
         "srq_step": (C.c_int, [P, P, I32, P, P, P, P, PP, P, P]),
         "srq_argmax": (C.c_int, [P, P, I32, I32, P]),
-        "srq_decoder_create": (C.c_int, [P, P, P, I32, I32, PP]),
+        "srq_decoder_create": (C.c_int, [P, P, P, I32, I32, I32, PP]),
         "srq_decoder_run": (C.c_int, [P, I32]),
         "srq_decoder_tokens": (C.c_int, [P, P, C.POINTER(I32)]),
         "srq_decoder_destroy": (C.c_int, [P]),
@@ -209,6 +211,11 @@ class DeviceBuffer:
             self.close()
         except Exception:
             pass
+
+
+def fill_normal(ex, buf, count, seed, scale):
+    """Device fill with f32(Normal()*scale) of RNG{seed} (see srq.h)."""
+    check(lib().srq_fill_normal(ex.h, buf.ptr, count, seed, scale))
 
 
 def packed_bytes(fmt, rows, cols):
@@ -350,7 +357,7 @@ class Model:
         w = None if want is None else np.array(want, np.uint8)
         out = np.zeros((sessions, self.config.vocab), np.float32)
         dev = C.c_void_p()
-        cflag = None if cancel is None else C.byref(cancel)
+        cflag = None if cancel is None else C.cast(C.pointer(cancel), C.c_void_p)
         check(lib().srq_step(self.ex.h, self.h, sessions, C.cast(handles, C.c_void_p), _np_ptr(lens), _np_ptr(tokens),
                              _np_ptr(w) if w is not None else None, C.byref(dev), _np_ptr(out), cflag))
         self.last_logits_ptr = dev.value
@@ -439,10 +446,11 @@ class Cache:
 class Decoder:
     """Graph-replayed greedy decode loop on one cache."""
 
-    def __init__(self, model, cache, first_token, max_steps):
+    def __init__(self, model, cache, first_token, max_steps, eager=False):
         self.model = model
         h = C.c_void_p()
-        check(lib().srq_decoder_create(model.ex.h, model.h, cache.h, int(first_token), max_steps, C.byref(h)))
+        check(lib().srq_decoder_create(model.ex.h, model.h, cache.h, int(first_token), max_steps, 1 if eager else 0,
+                                       C.byref(h)))
         self.h = h
         self.max_steps = max_steps
 

@@ -7,6 +7,7 @@
 // cmd/monolith/monolith.go.  Every GPU computation is a HIP kernel of this
 // library; there is no CPU fallback.
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -120,13 +121,19 @@ using namespace srq;
 // M:6062-6100).  Captured graphs point into a decoder's own workspace, so a
 // later step that grows the executor's workspace cannot invalidate them.
 struct Workspace {
-    DevBuf X, N, Q, A, T, H, W2, LOG, LOGC, meta, flags;
+    DevBuf X, N, Q, A, T, H, W2, LOG, LOGC, meta, flags, ATT;
     void release_all() {
-        for (DevBuf *b : {&X, &N, &Q, &A, &T, &H, &W2, &LOG, &LOGC, &meta, &flags}) release(*b);
+        for (DevBuf *b : {&X, &N, &Q, &A, &T, &H, &W2, &LOG, &LOGC, &meta, &flags, &ATT}) release(*b);
     }
 };
 
+// Handles are reference counted: a model holds its executor, a pool its
+// model, a cache its pool and a decoder its executor, model and cache, so
+// destroy calls may come in any order (Go finalizers, Python's collector)
+// without a handle outliving what it points to.  *_destroy drops the
+// caller's reference.
 struct srq_exec {
+    std::atomic<int> refs{1};
     int device = 0;
     hipStream_t stream = nullptr;
     int32_t *d_err = nullptr;  // [4] device error words
@@ -151,6 +158,7 @@ struct Layer {
 };
 
 struct srq_model {
+    std::atomic<int> refs{1};
     int device = 0;
     srq_exec *e = nullptr;
     srq_model_config c{};
@@ -167,6 +175,8 @@ struct srq_model {
 };
 
 struct srq_pool {
+    std::atomic<int> refs{1};
+    int device = 0;
     srq_model *m = nullptr;
     float *base = nullptr;
     int32_t max_pages = 0, reserved = 0;
@@ -175,6 +185,7 @@ struct srq_pool {
 };
 
 struct srq_cache {
+    std::atomic<int> refs{1};
     srq_pool *p = nullptr;
     int32_t pos = 0, reserve = 0;
     std::vector<int32_t> pages;
@@ -188,6 +199,9 @@ struct DeviceGuard {
     explicit DeviceGuard(int dev) {
         if (hipGetDevice(&prev) != hipSuccess) prev = -1;
         if (prev != dev) (void)hipSetDevice(dev);
+        // Drop any error left by an earlier best-effort call (a release on
+        // a teardown path) so launch checks report only their own errors.
+        (void)hipGetLastError();
     }
     ~DeviceGuard() {
         int cur = -1;
@@ -298,6 +312,9 @@ int run_linear(srq_exec *e, Workspace &ws, const srq_weight &w, const float *x, 
 
 }  // namespace
 
+static void exec_unref(srq_exec *e);
+static void model_unref(srq_model *m);
+
 // ====================================================================== ABI
 extern "C" {
 
@@ -362,7 +379,7 @@ int srq_exec_create(int device, srq_exec **out) {
     }
     if (hipMalloc((void **)&e->d_err, sizeof(int32_t) * 4) != hipSuccess ||
         hipHostMalloc((void **)&e->h_err, sizeof(int32_t) * 4) != hipSuccess) {
-        srq_exec_destroy(e);
+        exec_unref(e);
         return fail(SRQ_ENOMEM, "executor allocation failed");
     }
     SRQ_HIP(hipMemsetAsync(e->d_err, 0, sizeof(int32_t) * 4, e->stream));
@@ -371,8 +388,8 @@ int srq_exec_create(int device, srq_exec **out) {
     return SRQ_OK;
 }
 
-int srq_exec_destroy(srq_exec *e) {
-    if (!e) return SRQ_OK;
+static void exec_unref(srq_exec *e) {
+    if (!e || --e->refs > 0) return;
     DeviceGuard g(e->device);
     if (e->stream) (void)hipStreamSynchronize(e->stream);
     e->ws.release_all();
@@ -381,6 +398,10 @@ int srq_exec_destroy(srq_exec *e) {
     if (e->h_meta) (void)hipHostFree(e->h_meta);
     if (e->stream) (void)hipStreamDestroy(e->stream);
     delete e;
+}
+
+int srq_exec_destroy(srq_exec *e) {
+    exec_unref(e);
     return SRQ_OK;
 }
 
@@ -409,6 +430,15 @@ int srq_pack(srq_exec *e, srq_format fmt, int64_t rows, int64_t cols, const void
     DeviceGuard g(e->device);
     SRQ_CHECK(launch_pack(e->stream, fmt, rows, cols, src, dtype, values, scales, e->d_err));
     return check_err_flag(e, SRQ_ENONFINITE, "non-finite weight in pack source");
+}
+
+int srq_fill_normal(srq_exec *e, float *dst, int64_t count, uint64_t seed, double scale) {
+    if (!e || (count > 0 && !dst)) return fail(SRQ_EINVAL, "null pointer");
+    if (count < 0) return fail(SRQ_EINVAL, "negative count");
+    DeviceGuard g(e->device);
+    SRQ_CHECK(launch_fill_normal(e->stream, dst, count, seed, scale));
+    SRQ_HIP(hipStreamSynchronize(e->stream));
+    return SRQ_OK;
 }
 
 // ----------------------------------------------------------------- weights
@@ -496,6 +526,16 @@ int srq_linear(srq_exec *e, float *y, const float *x, const srq_weight *w, int32
     return SRQ_OK;
 }
 
+int srq_linear_enqueue(srq_exec *e, float *y, const float *x, const srq_weight *w, int32_t n) {
+    if (!e || !y || !x || !w) return fail(SRQ_EINVAL, "null pointer");
+    if (n < 1 || n > 1024) return fail(SRQ_EINVAL, "linear rows n=%d outside 1..1024", n);
+    const char *yb = (const char *)y, *xb = (const char *)x;
+    if (yb < xb + (size_t)n * w->cols * 4 && xb < yb + (size_t)n * w->rows * 4)
+        return fail(SRQ_EINVAL, "y overlaps x");
+    DeviceGuard g(e->device);
+    return run_linear(e, e->ws, *w, x, n, y, w->rows, nullptr, 0.0, nullptr);
+}
+
 // ------------------------------------------------------------------- model
 int srq_model_create(srq_exec *e, const srq_model_config *c, const char *weight_format, srq_model **out) {
     if (!e || !c || !weight_format || !out) return fail(SRQ_EINVAL, "null pointer");
@@ -512,6 +552,7 @@ int srq_model_create(srq_exec *e, const srq_model_config *c, const char *weight_
     srq_model *m = new srq_model();
     m->device = e->device;
     m->e = e;
+    e->refs++;
     m->c = *c;
     m->format = f;
     m->hd = c->dim / c->heads;
@@ -569,19 +610,26 @@ int srq_model_create(srq_exec *e, const srq_model_config *c, const char *weight_
         }
     }
     if (rc != SRQ_OK) {
-        srq_model_destroy(m);
+        model_unref(m);
         return rc;
     }
     *out = m;
     return SRQ_OK;
 }
 
-int srq_model_destroy(srq_model *m) {
-    if (!m) return SRQ_OK;
-    DeviceGuard g(m->device);
-    (void)hipDeviceSynchronize();
-    for (void *p : m->allocs) (void)hipFree(p);
+static void model_unref(srq_model *m) {
+    if (!m || --m->refs > 0) return;
+    {
+        DeviceGuard g(m->device);
+        (void)hipDeviceSynchronize();
+        for (void *p : m->allocs) (void)hipFree(p);
+    }
+    exec_unref(m->e);
     delete m;
+}
+
+int srq_model_destroy(srq_model *m) {
+    model_unref(m);
     return SRQ_OK;
 }
 
@@ -670,6 +718,7 @@ int srq_pool_create(srq_model *m, int32_t max_pages, srq_pool **out) {
     DeviceGuard g(m->device);
     srq_pool *p = new srq_pool();
     p->m = m;
+    p->device = m->device;
     p->max_pages = max_pages;
     p->page_elems = (int64_t)2 * kPageTokens * m->kvdim * m->c.layers;
     const size_t bytes = (size_t)max_pages * p->page_elems * 4;
@@ -683,16 +732,24 @@ int srq_pool_create(srq_model *m, int32_t max_pages, srq_pool **out) {
         return fail(SRQ_EDEVICE, "KV pool clear failed");
     }
     for (int32_t i = max_pages - 1; i >= 0; --i) p->free_list.push_back(i);
+    m->refs++;
     *out = p;
     return SRQ_OK;
 }
 
-int srq_pool_destroy(srq_pool *p) {
-    if (!p) return SRQ_OK;
-    DeviceGuard g(p->m->device);
-    (void)hipDeviceSynchronize();
-    if (p->base) (void)hipFree(p->base);
+static void pool_unref(srq_pool *p) {
+    if (!p || --p->refs > 0) return;
+    {
+        DeviceGuard g(p->device);
+        (void)hipDeviceSynchronize();
+        if (p->base) (void)hipFree(p->base);
+    }
+    model_unref(p->m);
     delete p;
+}
+
+int srq_pool_destroy(srq_pool *p) {
+    pool_unref(p);
     return SRQ_OK;
 }
 
@@ -708,18 +765,25 @@ int srq_cache_create(srq_pool *p, int32_t reserve_pages, srq_cache **out) {
     c->p = p;
     c->reserve = reserve_pages;
     p->reserved += reserve_pages;
+    p->refs++;
     *out = c;
     return SRQ_OK;
 }
 
+static void cache_unref(srq_cache *c) {
+    if (!c || --c->refs > 0) return;
+    for (int32_t pg : c->pages) c->p->free_list.push_back(pg);
+    c->p->reserved -= c->reserve;
+    pool_unref(c->p);
+    delete c;
+}
+
+// Returns the cache's pages to its pool (Close, M:6044-6061) once no
+// decoder uses it any more.
 int srq_cache_destroy(srq_cache *c) {
     if (!c) return SRQ_OK;
-    if (!c->released) {
-        for (int32_t pg : c->pages) c->p->free_list.push_back(pg);
-        c->p->reserved -= c->reserve;
-        c->released = true;
-    }
-    delete c;
+    c->released = true;
+    cache_unref(c);
     return SRQ_OK;
 }
 
@@ -879,7 +943,7 @@ int enqueue_layers(srq_exec *e, Workspace &ws, srq_model *m, srq_pool *pool, int
         at.head_dim = m->hd;
         at.max_len = max_len;
         at.meta = meta;
-        SRQ_CHECK(launch_attention(e->stream, at));
+        SRQ_CHECK(launch_attention(e->stream, at, as<float>(ws.ATT)));
         // O projection + residual (M:6398-6400).
         SRQ_CHECK(run_linear(e, ws, L.o, A, n, X, d, nullptr, 0.0, X));
         if (!use_gemm) {
@@ -922,7 +986,7 @@ int enqueue_head(srq_exec *e, Workspace &ws, srq_model *m, const float *rows, in
     return run_linear(e, ws, head, rows, heads, LOGC, m->c.vocab, m->final_norm, m->c.norm_eps, nullptr);
 }
 
-int ensure_workspace(srq_exec *e, Workspace &ws, srq_model *m, int32_t n, int32_t sessions) {
+int ensure_workspace(srq_exec *e, Workspace &ws, srq_model *m, int32_t n, int32_t sessions, int32_t max_len) {
     const int64_t d = m->c.dim, kd = m->kvdim, H = m->c.hidden, V = m->c.vocab;
     const size_t nd = (size_t)n * d * 4;
     SRQ_CHECK(ensure(ws.X, nd, e->stream));
@@ -934,6 +998,7 @@ int ensure_workspace(srq_exec *e, Workspace &ws, srq_model *m, int32_t n, int32_
     SRQ_CHECK(ensure(ws.W2, (size_t)n * std::max<int64_t>(d + 2 * kd, 2 * H) * 4, e->stream));
     SRQ_CHECK(ensure(ws.LOGC, (size_t)sessions * V * 4, e->stream));
     SRQ_CHECK(ensure(ws.LOG, (size_t)sessions * V * 4, e->stream));
+    SRQ_CHECK(ensure(ws.ATT, attention_scratch_bytes(n, m->c.heads, m->hd, max_len), e->stream));
     return SRQ_OK;
 }
 
@@ -952,7 +1017,7 @@ extern "C" int srq_step(srq_exec *e, srq_model *m, int32_t sessions, srq_cache *
     for (int32_t i = 1; i < sessions; ++i)
         if (caches[i]->p != pool) return fail(SRQ_EINVAL, "sessions of one step must share a KV pool");
     Workspace &ws = e->ws;
-    SRQ_CHECK(ensure_workspace(e, ws, m, n, sessions));
+    SRQ_CHECK(ensure_workspace(e, ws, m, n, sessions, max_pos));
     const int32_t pt_stride = (m->c.context + kPageTokens - 1) / kPageTokens;
     const size_t words = meta_words(n, sessions, pt_stride);
     SRQ_CHECK(ensure(ws.meta, words * 4, e->stream));
@@ -1038,14 +1103,34 @@ struct srq_decoder {
     Workspace ws;             // private: the captured graph points into it
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
+    bool eager = false;
 };
 
 extern "C" {
 
 int srq_decoder_destroy(srq_decoder *d);
 
+static int enqueue_decode_step(srq_decoder *d) {
+    srq_exec *e = d->e;
+    srq_model *m = d->m;
+    StepMeta dm{};
+    int32_t *pos = d->dbuf, *sess = d->dbuf + 1, *counter = d->dbuf + 2, *embed_id = d->dbuf + 3;
+    int32_t *token = d->dbuf + 4, *err = d->dbuf + 5, *pt = d->dbuf + 6, *outbuf = d->dbuf + 6 + d->pt_stride;
+    dm.pos = pos;
+    dm.sess = sess;
+    dm.pages = pt;
+    dm.pt_stride = d->pt_stride;
+    Workspace &ws = d->ws;
+    SRQ_CHECK(launch_dequant_rows(e->stream, m->embed.fmt, m->c.dim, m->embed.values, m->embed.scales, embed_id, 1,
+                                  as<float>(ws.X)));
+    SRQ_CHECK(enqueue_layers(e, ws, m, d->c->p, 1, d->start_pos + d->max_steps, dm, nullptr));
+    SRQ_CHECK(enqueue_head(e, ws, m, as<float>(ws.X), 1));
+    SRQ_CHECK(launch_argmax(e->stream, as<float>(ws.LOGC), 1, m->c.vocab, token, err));
+    return launch_advance(e->stream, pos, token, outbuf, counter, embed_id);
+}
+
 int srq_decoder_create(srq_exec *e, srq_model *m, srq_cache *c, int32_t first_token, int32_t max_steps,
-                       srq_decoder **out) {
+                       int32_t flags, srq_decoder **out) {
     if (!e || !m || !c || !out) return fail(SRQ_EINVAL, "null pointer");
     *out = nullptr;
     if (c->released || c->p->m != m) return fail(SRQ_EINVAL, "foreign or released KV cache");
@@ -1060,6 +1145,9 @@ int srq_decoder_create(srq_exec *e, srq_model *m, srq_cache *c, int32_t first_to
     d->e = e;
     d->m = m;
     d->c = c;
+    e->refs++;
+    m->refs++;
+    c->refs++;
     d->start_pos = c->pos;
     d->max_steps = max_steps;
     d->pt_stride = (m->c.context + kPageTokens - 1) / kPageTokens;
@@ -1069,7 +1157,8 @@ int srq_decoder_create(srq_exec *e, srq_model *m, srq_cache *c, int32_t first_to
     }
     const size_t words = 6 + (size_t)d->pt_stride + (size_t)max_steps;
     if (hipMalloc((void **)&d->dbuf, words * 4) != hipSuccess) {
-        delete d;
+        d->dbuf = nullptr;
+        srq_decoder_destroy(d);
         return fail(SRQ_ENOMEM, "decoder allocation failed");
     }
     std::vector<int32_t> h(words, 0);
@@ -1078,7 +1167,7 @@ int srq_decoder_create(srq_exec *e, srq_model *m, srq_cache *c, int32_t first_to
     h[2] = 0;
     h[3] = first_token;
     for (int32_t p = 0; p < d->pt_stride; ++p) h[6 + p] = p < (int32_t)c->pages.size() ? c->pages[p] : 0;
-    int rc = ensure_workspace(e, d->ws, m, 1, 1);
+    int rc = ensure_workspace(e, d->ws, m, 1, 1, end);
     if (rc == SRQ_OK && hipMemcpy(d->dbuf, h.data(), words * 4, hipMemcpyHostToDevice) != hipSuccess)
         rc = fail(SRQ_EDEVICE, "decoder upload failed");
     if (rc == SRQ_OK && hipStreamSynchronize(e->stream) != hipSuccess) rc = fail(SRQ_EDEVICE, "sync failed");
@@ -1086,33 +1175,24 @@ int srq_decoder_create(srq_exec *e, srq_model *m, srq_cache *c, int32_t first_to
         srq_decoder_destroy(d);
         return rc;
     }
-    // One decode step, captured once and replayed: embed -> layers -> final
-    // norm + head -> argmax -> record token, advance position.
-    StepMeta dm{};
-    int32_t *pos = d->dbuf, *sess = d->dbuf + 1, *counter = d->dbuf + 2, *embed_id = d->dbuf + 3;
-    int32_t *token = d->dbuf + 4, *err = d->dbuf + 5, *pt = d->dbuf + 6, *outbuf = d->dbuf + 6 + d->pt_stride;
-    dm.pos = pos;
-    dm.sess = sess;
-    dm.pages = pt;
-    dm.pt_stride = d->pt_stride;
-    if (hipStreamBeginCapture(e->stream, hipStreamCaptureModeThreadLocal) != hipSuccess) {
-        srq_decoder_destroy(d);
-        return fail(SRQ_EDEVICE, "graph capture failed to start");
-    }
-    Workspace &ws = d->ws;
-    rc = launch_dequant_rows(e->stream, m->embed.fmt, m->c.dim, m->embed.values, m->embed.scales, embed_id, 1,
-                             as<float>(ws.X));
-    if (rc == SRQ_OK) rc = enqueue_layers(e, ws, m, c->p, 1, end, dm, nullptr);
-    if (rc == SRQ_OK) rc = enqueue_head(e, ws, m, as<float>(ws.X), 1);
-    if (rc == SRQ_OK) rc = launch_argmax(e->stream, as<float>(ws.LOGC), 1, m->c.vocab, token, err);
-    if (rc == SRQ_OK) rc = launch_advance(e->stream, pos, token, outbuf, counter, embed_id);
-    hipError_t ce = hipStreamEndCapture(e->stream, &d->graph);
-    if (rc == SRQ_OK && ce != hipSuccess) rc = fail(SRQ_EDEVICE, "graph capture failed: %s", hipGetErrorString(ce));
-    if (rc == SRQ_OK && hipGraphInstantiate(&d->exec, d->graph, nullptr, nullptr, 0) != hipSuccess)
-        rc = fail(SRQ_EDEVICE, "graph instantiation failed");
-    if (rc != SRQ_OK) {
-        srq_decoder_destroy(d);
-        return rc;
+    // One decode step: embed -> layers -> final norm + head -> argmax ->
+    // record token, advance position.  Captured once as a HIP graph and
+    // replayed, unless the caller asked for eager launches.
+    d->eager = (flags & SRQ_DECODER_EAGER) != 0;
+    if (!d->eager) {
+        if (hipStreamBeginCapture(e->stream, hipStreamCaptureModeThreadLocal) != hipSuccess) {
+            srq_decoder_destroy(d);
+            return fail(SRQ_EDEVICE, "graph capture failed to start");
+        }
+        rc = enqueue_decode_step(d);
+        hipError_t ce = hipStreamEndCapture(e->stream, &d->graph);
+        if (rc == SRQ_OK && ce != hipSuccess) rc = fail(SRQ_EDEVICE, "graph capture failed: %s", hipGetErrorString(ce));
+        if (rc == SRQ_OK && hipGraphInstantiate(&d->exec, d->graph, nullptr, nullptr, 0) != hipSuccess)
+            rc = fail(SRQ_EDEVICE, "graph instantiation failed");
+        if (rc != SRQ_OK) {
+            srq_decoder_destroy(d);
+            return rc;
+        }
     }
     *out = d;
     return SRQ_OK;
@@ -1124,7 +1204,12 @@ int srq_decoder_run(srq_decoder *d, int32_t steps) {
     if (!d) return fail(SRQ_EINVAL, "null decoder");
     if (steps < 0 || d->steps + steps > d->max_steps) return fail(SRQ_ERANGE, "decoder step budget exceeded");
     DeviceGuard g(d->e->device);
-    for (int32_t i = 0; i < steps; ++i) SRQ_HIP(hipGraphLaunch(d->exec, d->e->stream));
+    for (int32_t i = 0; i < steps; ++i) {
+        if (d->eager)
+            SRQ_CHECK(enqueue_decode_step(d));
+        else
+            SRQ_HIP(hipGraphLaunch(d->exec, d->e->stream));
+    }
     d->steps += steps;
     return SRQ_OK;
 }
@@ -1146,12 +1231,17 @@ int srq_decoder_tokens(srq_decoder *d, int32_t *out, int32_t *count) {
 
 int srq_decoder_destroy(srq_decoder *d) {
     if (!d) return SRQ_OK;
-    DeviceGuard g(d->e->device);
-    (void)hipStreamSynchronize(d->e->stream);
-    if (d->exec) (void)hipGraphExecDestroy(d->exec);
-    if (d->graph) (void)hipGraphDestroy(d->graph);
-    if (d->dbuf) (void)hipFree(d->dbuf);
-    d->ws.release_all();
+    {
+        DeviceGuard g(d->e->device);
+        (void)hipStreamSynchronize(d->e->stream);
+        if (d->exec) (void)hipGraphExecDestroy(d->exec);
+        if (d->graph) (void)hipGraphDestroy(d->graph);
+        if (d->dbuf) (void)hipFree(d->dbuf);
+        d->ws.release_all();
+    }
+    cache_unref(d->c);
+    model_unref(d->m);
+    exec_unref(d->e);
     delete d;
     return SRQ_OK;
 }
@@ -1176,7 +1266,7 @@ int srq_generate_greedy(srq_exec *e, srq_model *m, srq_cache *c, const int32_t *
     *produced = 1;
     if (count == 1 || first == eos) return SRQ_OK;
     srq_decoder *d = nullptr;
-    SRQ_CHECK(srq_decoder_create(e, m, c, first, count - 1, &d));
+    SRQ_CHECK(srq_decoder_create(e, m, c, first, count - 1, 0, &d));
     int rc = SRQ_OK;
     int32_t done = 0;
     const int32_t seg = eos >= 0 ? 16 : count - 1;

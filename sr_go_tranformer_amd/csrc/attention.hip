@@ -3,22 +3,29 @@
 // attend (cmd/monolith/monolith.go M:5293-5352) for every (row, query head)
 // of a step (attentionRange M:6131-6147): scores = f32 dot(q, k_s) *
 // f32(1/sqrt(hd)) over positions 0..pos of the row's own cache (earlier rows
-// of the same chunk included, their K/V already written), max, FP64 sum of
-// exp(score - max), lse = max + log(sum), p = f32(exp(score - lse)),
-// out = sum_s p * v_s.  Query head h reads KV head h / (heads/kv_heads).
-//
+// of the same chunk included: their K/V were written first), max, FP64 sum
+// of exp(score - max), lse = max + log(sum), out = sum_s p_s v_s with
+// p_s = exp(score_s - lse).  Query head h reads KV head h / (heads/kv_heads).
 // Pages are [layer][K 32 x kvdim | V 32 x kvdim] (M:6038-6043); a row's page
-// table maps position/32 to a page of the pool.
+// table maps position/32 to a pool page.
 //
-// One workgroup per (row, head).  Scores live in LDS (up to the model
-// context, 32768 positions = 128 KiB).  Keys are scored by 16-lane groups
-// (4 keys per wave at a time, lanes strided over the head dimension, a
-// 16-lane xor tree); the value pass gives each thread one output element
-// and a contiguous range of positions, combined in a fixed order.
+// Split over positions (flash-decoding): workgroup (row, kv head, split)
+// scores kSplit positions for all query heads of its GQA group, so each K/V
+// row is read once per group.  It keeps the split's max m_i, FP64 sum
+// l_i = sum exp(score - m_i) and o_i = sum f32(exp(score - m_i)) v_s.  The
+// combine kernel forms lse = M + log(sum_i l_i exp(m_i - M)) and
+// out = sum_i f32(exp(m_i - lse)) o_i, which equals the reference's
+// sum_s exp(score_s - lse) v_s up to f32 rounding of the factors.
+#include <cfloat>
+
 #include "srq_internal.h"
 
 namespace srq {
 namespace {
+
+constexpr int kSplit = 64;     // positions per split (two pages)
+constexpr int kMaxGroup = 8;   // query heads per KV head handled together
+constexpr int kMaxHd = 256;
 
 __device__ __forceinline__ const float *kv_row(const RowMeta &m, int sess, int pos, int kvdim, int which) {
     const int page = m.pages[(int64_t)sess * m.pt_stride + pos / kPageTokens];
@@ -26,97 +33,296 @@ __device__ __forceinline__ const float *kv_row(const RowMeta &m, int sess, int p
            (int64_t)which * kPageTokens * kvdim + (int64_t)(pos % kPageTokens) * kvdim;
 }
 
-__global__ __launch_bounds__(256) void attention_kernel(const AttnArgs A) {
-    extern __shared__ float scores[];
-    __shared__ float qs[256];
-    __shared__ float redf[4];
-    __shared__ double redd[4];
-    __shared__ float part[256];
+// Partials: [row][head][split] -> {m, l(double as 2 floats), o[hd]}.
+__device__ __forceinline__ float *partial(float *base, int row, int h, int sp, int heads, int nsplit, int hd) {
+    return base + (((int64_t)row * heads + h) * nsplit + sp) * (hd + 4);
+}
 
-    const int row = blockIdx.x, h = blockIdx.y;
+__global__ __launch_bounds__(256) void attn_split_kernel(const AttnArgs A, float *__restrict__ part, int nsplit) {
+    __shared__ float qs[kMaxGroup * kMaxHd];
+    __shared__ float sc[kMaxGroup][kSplit];
+    __shared__ float mx[kMaxGroup];
+    __shared__ float ov[2][kMaxGroup * kMaxHd];
+
+    const int row = blockIdx.x, kh = blockIdx.y, sp = blockIdx.z;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int hd = A.head_dim, kvdim = A.kv_heads * hd;
-    const int kh = h / (A.heads / A.kv_heads);
+    const int hd = A.head_dim, kvdim = A.kv_heads * hd, G = A.heads / A.kv_heads;
     const int pos = A.meta.pos[row], sess = A.meta.sess[row];
-    const int len = pos + 1;
-    const float *q = A.q + (int64_t)row * A.heads * hd + (int64_t)h * hd;
-    for (int j = tid; j < hd; j += 256) qs[j] = q[j];
+    const int len = pos + 1, s0 = sp * kSplit, s1 = min(len, s0 + kSplit), ns = s1 - s0;
+    if (ns <= 0) {
+        // Empty split: contributes nothing to the combine.
+        for (int i = tid; i < G * (hd + 4); i += 256) {
+            const int g = i / (hd + 4), k = i - g * (hd + 4);
+            float *p = partial(part, row, kh * G + g, sp, A.heads, nsplit, hd);
+            p[k] = k == 0 ? -FLT_MAX : 0.0f;
+        }
+        return;
+    }
+    for (int i = tid; i < G * hd; i += 256) {
+        const int g = i / hd, j = i - g * hd;
+        qs[i] = A.q[(int64_t)row * A.heads * hd + (int64_t)(kh * G + g) * hd + j];
+    }
     __syncthreads();
     const float scale = (float)(1.0 / sqrt((double)hd));
 
-    // ---- scores -----------------------------------------------------------
+    // ---- scores: one 16-lane group per key, all G heads of the group ----
     const int sub = lane >> 4, l16 = lane & 15;
-    float mx = -3.402823466e38f;
-    for (int s0 = wave * 4; s0 < len; s0 += 16) {
-        const int s = s0 + sub;
-        float dot = 0.0f;
-        if (s < len) {
-            const float *k = kv_row(A.meta, sess, s, kvdim, 0) + (int64_t)kh * hd;
-            for (int j = l16; j < hd; j += 16) dot = __builtin_fmaf(qs[j], k[j], dot);
+    for (int s = wave * 4 + sub; s < ((ns + 15) / 16) * 16; s += 16) {
+        float dot[kMaxGroup];
+#pragma unroll
+        for (int g = 0; g < kMaxGroup; ++g) dot[g] = 0.0f;
+        if (s < ns) {
+            const float *k = kv_row(A.meta, sess, s0 + s, kvdim, 0) + (int64_t)kh * hd;
+            for (int j = l16; j < hd; j += 16) {
+                const float kj = k[j];
+#pragma unroll
+                for (int g = 0; g < kMaxGroup; ++g)
+                    if (g < G) dot[g] = __builtin_fmaf(qs[g * hd + j], kj, dot[g]);
+            }
         }
 #pragma unroll
-        for (int o = 8; o > 0; o >>= 1) dot += __shfl_xor(dot, o, 64);
-        if (s < len) {
-            const float sc = dot * scale;
-            if (l16 == 0) scores[s] = sc;
-            mx = fmaxf(mx, sc);
+        for (int g = 0; g < kMaxGroup; ++g) {
+            float d = dot[g];
+#pragma unroll
+            for (int o = 8; o > 0; o >>= 1) d += __shfl_xor(d, o, 64);
+            if (g < G && s < ns && l16 == 0) sc[g][s] = d * scale;
         }
     }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
-    if (lane == 0) redf[wave] = mx;
-    __syncthreads();
-    mx = fmaxf(fmaxf(redf[0], redf[1]), fmaxf(redf[2], redf[3]));
-
-    // ---- FP64 normaliser ----------------------------------------------------
-    double sum = 0.0;
-    for (int s = tid; s < len; s += 256) sum += exp((double)scores[s] - (double)mx);
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o, 64);
-    if (lane == 0) redd[wave] = sum;
-    __syncthreads();
-    sum = redd[0] + redd[1] + redd[2] + redd[3];
-    const double lse = (double)mx + log(sum);
-    for (int s = tid; s < len; s += 256) scores[s] = (float)exp((double)scores[s] - lse);
     __syncthreads();
 
-    // ---- values ---------------------------------------------------------------
-    const int nparts = 256 / hd;  // hd <= 256
-    const int j = tid % hd, pidx = tid / hd;
-    float acc = 0.0f;
-    if (pidx < nparts) {
-        const int per = (len + nparts - 1) / nparts;
-        const int lo = pidx * per, hi = min(len, lo + per);
+    // ---- per-head split max and FP64 sum ---------------------------------
+    if (wave == 0) {
+        for (int g = 0; g < G; ++g) {
+            float m = -FLT_MAX;
+            for (int s = lane; s < ns; s += 64) m = fmaxf(m, sc[g][s]);
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+            double l = 0.0;
+            for (int s = lane; s < ns; s += 64) {
+                const double e = exp((double)sc[g][s] - (double)m);
+                l += e;
+                sc[g][s] = (float)e;  // weight of position s inside this split
+            }
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) l += __shfl_xor(l, o, 64);
+            if (lane == 0) {
+                mx[g] = m;
+                float *p = partial(part, row, kh * G + g, sp, A.heads, nsplit, hd);
+                p[0] = m;
+                *(double *)(p + 2) = l;
+            }
+        }
+    }
+    __syncthreads();
+
+    // ---- o_i = sum_s w_s v_s: thread = (half of the keys, dim j) ----------
+    const int halfk = tid / 128, j = tid & 127;
+    for (int jj = j; jj < hd; jj += 128) {
+        float acc[kMaxGroup];
+#pragma unroll
+        for (int g = 0; g < kMaxGroup; ++g) acc[g] = 0.0f;
+        const int mid = (ns + 1) / 2;
+        const int lo = halfk ? mid : 0, hi = halfk ? ns : mid;
         for (int s = lo; s < hi; ++s) {
-            const float *v = kv_row(A.meta, sess, s, kvdim, 1) + (int64_t)kh * hd;
-            acc = __builtin_fmaf(scores[s], v[j], acc);
+            const float vj = kv_row(A.meta, sess, s0 + s, kvdim, 1)[(int64_t)kh * hd + jj];
+#pragma unroll
+            for (int g = 0; g < kMaxGroup; ++g)
+                if (g < G) acc[g] = __builtin_fmaf(sc[g][s], vj, acc[g]);
         }
-        part[tid] = acc;
+#pragma unroll
+        for (int g = 0; g < kMaxGroup; ++g)
+            if (g < G) ov[halfk][g * hd + jj] = acc[g];
     }
     __syncthreads();
-    if (tid < hd) {
+    for (int i = tid; i < G * hd; i += 256) {
+        const int g = i / hd, jj = i - g * hd;
+        float *p = partial(part, row, kh * G + g, sp, A.heads, nsplit, hd);
+        p[4 + jj] = ov[0][i] + ov[1][i];
+    }
+}
+
+
+// Fast split kernel for head_dim 64 / 128: every K and V element of the
+// split is loaded by exactly one thread with independent float4 loads, so a
+// split costs one round of memory latency per pass.
+//  scores: thread t -> key t/4 of the split, dims [(t%4)*HD/4, +HD/4)
+//  values: thread t -> dims 4*(t%(HD/4)) .. +3, keys t/(HD/4) + KG*i
+template <int HD>
+__global__ __launch_bounds__(256) void attn_split_fast_kernel(const AttnArgs A, float *__restrict__ part,
+                                                              int nsplit) {
+    constexpr int QD = HD / 4;           // dims per scoring thread
+    constexpr int DG = HD / 4;           // float4 dim groups in the value pass
+    constexpr int KG = 256 / DG;         // key groups in the value pass
+    constexpr int KPG = kSplit / KG;     // keys per value thread
+    __shared__ float qs[kMaxGroup * HD];
+    __shared__ float sc[kMaxGroup][kSplit];
+    __shared__ float4 red[KG][DG];
+
+    const int row = blockIdx.x, kh = blockIdx.y, sp = blockIdx.z;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int kvdim = A.kv_heads * HD, G = A.heads / A.kv_heads;
+    const int pos = A.meta.pos[row], sess = A.meta.sess[row];
+    const int len = pos + 1, s0 = sp * kSplit, s1 = min(len, s0 + kSplit), ns = s1 - s0;
+    if (ns <= 0) {
+        for (int i = tid; i < G * (HD + 4); i += 256) {
+            const int g = i / (HD + 4), k = i - g * (HD + 4);
+            float *p = partial(part, row, kh * G + g, sp, A.heads, nsplit, HD);
+            p[k] = k == 0 ? -FLT_MAX : 0.0f;
+        }
+        return;
+    }
+    for (int i = tid; i < G * HD; i += 256) {
+        const int g = i / HD, j = i - g * HD;
+        qs[i] = A.q[(int64_t)row * A.heads * HD + (int64_t)(kh * G + g) * HD + j];
+    }
+    __syncthreads();
+    const float scale = (float)(1.0 / sqrt((double)HD));
+
+    // ---- scores -------------------------------------------------------------
+    {
+        const int s = tid >> 2, part4 = tid & 3;
+        const int sk = s < ns ? s : 0;  // clamp: load a valid row, drop below
+        const float *k = kv_row(A.meta, sess, s0 + sk, kvdim, 0) + (int64_t)kh * HD + part4 * QD;
+        float4 kr[QD / 4];
+#pragma unroll
+        for (int u = 0; u < QD / 4; ++u) kr[u] = ((const float4 *)k)[u];
+#pragma unroll
+        for (int g = 0; g < kMaxGroup; ++g) {
+            if (g >= G) break;
+            const float *q = qs + g * HD + part4 * QD;
+            float d = 0.0f;
+#pragma unroll
+            for (int u = 0; u < QD / 4; ++u) {
+                d = __builtin_fmaf(q[4 * u + 0], kr[u].x, d);
+                d = __builtin_fmaf(q[4 * u + 1], kr[u].y, d);
+                d = __builtin_fmaf(q[4 * u + 2], kr[u].z, d);
+                d = __builtin_fmaf(q[4 * u + 3], kr[u].w, d);
+            }
+            d += __shfl_xor(d, 1, 64);
+            d += __shfl_xor(d, 2, 64);
+            if (part4 == 0 && s < ns) sc[g][s] = d * scale;
+        }
+    }
+    __syncthreads();
+
+    // ---- per-head split max and FP64 sum (one wave per head) ----------------
+    const int wave = tid >> 6;
+    for (int g = wave; g < G; g += 4) {
+        float m = -FLT_MAX;
+        if (lane < ns) m = sc[g][lane];
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+        double e = 0.0;
+        if (lane < ns) {
+            e = exp((double)sc[g][lane] - (double)m);
+            sc[g][lane] = (float)e;
+        }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) e += __shfl_xor(e, o, 64);
+        if (lane == 0) {
+            float *p = partial(part, row, kh * G + g, sp, A.heads, nsplit, HD);
+            p[0] = m;
+            *(double *)(p + 2) = e;
+        }
+    }
+    __syncthreads();
+
+    // ---- values ------------------------------------------------------------
+    const int dg = tid % DG, kg = tid / DG;
+    float4 vr[KPG];
+#pragma unroll
+    for (int i = 0; i < KPG; ++i) {
+        const int s = kg + KG * i;
+        const int sk = s < ns ? s : 0;
+        vr[i] = ((const float4 *)(kv_row(A.meta, sess, s0 + sk, kvdim, 1) + (int64_t)kh * HD))[dg];
+    }
+    for (int g = 0; g < G; ++g) {
+        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int i = 0; i < KPG; ++i) {
+            const int s = kg + KG * i;
+            const float w = s < ns ? sc[g][s] : 0.0f;
+            acc.x = __builtin_fmaf(w, vr[i].x, acc.x);
+            acc.y = __builtin_fmaf(w, vr[i].y, acc.y);
+            acc.z = __builtin_fmaf(w, vr[i].z, acc.z);
+            acc.w = __builtin_fmaf(w, vr[i].w, acc.w);
+        }
+        red[kg][dg] = acc;
+        __syncthreads();
+        if (tid < DG) {
+            float4 t = red[0][tid];
+            for (int k2 = 1; k2 < KG; ++k2) {
+                const float4 u = red[k2][tid];
+                t.x += u.x, t.y += u.y, t.z += u.z, t.w += u.w;
+            }
+            float *p = partial(part, row, kh * G + g, sp, A.heads, nsplit, HD);
+            ((float4 *)(p + 4))[tid] = t;
+        }
+        __syncthreads();
+    }
+}
+
+// lse and the weighted sum of split partials for one (row, head).
+__global__ __launch_bounds__(256) void attn_combine_kernel(const AttnArgs A, const float *__restrict__ part,
+                                                           int nsplit) {
+    __shared__ float cf[1024];
+    __shared__ double red[4];
+    const int row = blockIdx.x, h = blockIdx.y, tid = threadIdx.x, hd = A.head_dim;
+    const int len = A.meta.pos[row] + 1;
+    const int used = min(nsplit, (len + kSplit - 1) / kSplit);
+    float M = -FLT_MAX;
+    for (int i = 0; i < used; ++i) M = fmaxf(M, partial((float *)part, row, h, i, A.heads, nsplit, hd)[0]);
+    double l = 0.0;
+    for (int i = tid; i < used; i += 256) {
+        const float *p = partial((float *)part, row, h, i, A.heads, nsplit, hd);
+        l += *(const double *)(p + 2) * exp((double)p[0] - (double)M);
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) l += __shfl_xor(l, o, 64);
+    if ((tid & 63) == 0) red[tid >> 6] = l;
+    __syncthreads();
+    l = red[0] + red[1] + red[2] + red[3];
+    const double lse = (double)M + log(l);
+    for (int i = tid; i < used; i += 256) {
+        const float *p = partial((float *)part, row, h, i, A.heads, nsplit, hd);
+        cf[i] = (float)exp((double)p[0] - lse);
+    }
+    __syncthreads();
+    for (int j = tid; j < hd; j += 256) {
         float o = 0.0f;
-        for (int p = 0; p < nparts; ++p) o += part[p * hd + tid];
-        A.out[(int64_t)row * A.heads * hd + (int64_t)h * hd + tid] = o;
+        for (int i = 0; i < used; ++i) o = __builtin_fmaf(cf[i], partial((float *)part, row, h, i, A.heads, nsplit, hd)[4 + j], o);
+        A.out[(int64_t)row * A.heads * hd + (int64_t)h * hd + j] = o;
     }
 }
 
 }  // namespace
 
-int launch_attention(hipStream_t s, const AttnArgs &a) {
+int attention_splits(int32_t max_len) { return (max_len + kSplit - 1) / kSplit; }
+
+size_t attention_scratch_bytes(int32_t n, int32_t heads, int32_t head_dim, int32_t max_len) {
+    return (size_t)n * heads * attention_splits(max_len) * (head_dim + 4) * sizeof(float);
+}
+
+int launch_attention(hipStream_t s, const AttnArgs &a, float *scratch) {
     if (a.n <= 0) return SRQ_OK;
-    if (a.head_dim > 256 || a.head_dim < 1) return fail(SRQ_EINVAL, "attention: head_dim %d unsupported", a.head_dim);
-    const size_t lds = (size_t)(a.max_len > 0 ? a.max_len : 1) * sizeof(float);
-    if (lds > 140 * 1024) return fail(SRQ_EINVAL, "attention: %d positions exceed LDS", a.max_len);
-    attention_kernel<<<dim3(a.n, a.heads), 256, lds, s>>>(a);
+    if (a.head_dim > kMaxHd || a.head_dim < 1) return fail(SRQ_EINVAL, "attention: head_dim %d unsupported", a.head_dim);
+    const int G = a.heads / a.kv_heads;
+    if (G > kMaxGroup) return fail(SRQ_EINVAL, "attention: %d query heads per KV head exceed %d", G, kMaxGroup);
+    const int nsplit = attention_splits(a.max_len);
+    if (nsplit > 1024) return fail(SRQ_EINVAL, "attention: %d positions exceed the split table", a.max_len);
+    const dim3 grid(a.n, a.kv_heads, nsplit);
+    if (a.head_dim == 128)
+        attn_split_fast_kernel<128><<<grid, 256, 0, s>>>(a, scratch, nsplit);
+    else if (a.head_dim == 64)
+        attn_split_fast_kernel<64><<<grid, 256, 0, s>>>(a, scratch, nsplit);
+    else
+        attn_split_kernel<<<grid, 256, 0, s>>>(a, scratch, nsplit);
+    SRQ_HIP(hipGetLastError());
+    attn_combine_kernel<<<dim3(a.n, a.heads), 256, 0, s>>>(a, scratch, nsplit);
     SRQ_HIP(hipGetLastError());
     return SRQ_OK;
 }
 
-int attention_prepare() {
-    SRQ_HIP(hipFuncSetAttribute((const void *)attention_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                140 * 1024));
-    return SRQ_OK;
-}
+int attention_prepare() { return SRQ_OK; }
 
 }  // namespace srq

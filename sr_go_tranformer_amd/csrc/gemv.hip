@@ -25,6 +25,8 @@
 //    row's slot, so results are batch invariant and deterministic.
 //  - Rows holding any |x| > f32(MaxFloat32/(2*64*127)) are recomputed in
 //    FP64 (Sum_g f64(scale_g) * Sum_j f64(x_j) f64(w_j), M:4356-4382).
+#include <cstdlib>
+
 #include "srq_internal.h"
 
 namespace srq {
@@ -125,37 +127,56 @@ struct Smem {
     int any_wide;
 };
 
-template <int FMT, bool FAST, int NB, int EPI>
-__global__ __launch_bounds__(kThreads) void gemv_kernel(const GemvArgs A) {
-    using L = Lay<FMT, FAST>;
-    constexpr int E = L::E, CW = L::CW;
-    extern __shared__ float xs[];
-    __shared__ Smem sm;
-
+// Stage the n activation rows of x into LDS (permuted layout), apply the
+// fused RMSNorm when NORM, and flag rows that need the FP64 path.  Ends with
+// a barrier; every thread of the workgroup must call it.
+template <int E, int CW, int NB, bool NORM>
+__device__ __forceinline__ void stage_x(const GemvArgs &A, float *xs, Smem &sm, int ld) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int64_t cols = A.cols;
-    const int nch = (int)((cols + CW - 1) / CW);
-    const int ld = nch * CW;  // LDS words per activation row
-
-    // ---- stage x (and RMSNorm) ------------------------------------------
     if (tid < NB) sm.wide[tid] = 0;
     if (tid == 0) sm.any_wide = 0;
+    // Vector path: 4 consecutive columns share l and q, so they are 4
+    // consecutive LDS words too.  Loads are issued 8 deep before the stores.
+    const bool vec = (cols & 3) == 0 && (((uintptr_t)A.x) & 15) == 0 && (E & 3) == 0;
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
         double ss = 0.0;
         const float *xb = A.x + (int64_t)b * cols;
-        for (int c = tid; c < ld; c += kThreads) {
-            float v = (b < A.n && c < cols) ? xb[c] : 0.0f;
-            xs[b * ld + xidx<E, CW>(c)] = v;
-            ss += (double)v * (double)v;
+        if (vec) {
+            constexpr int U = 8;
+            for (int c0 = tid * 4; c0 < ld; c0 += kThreads * 4 * U) {
+                float4 t[U];
+#pragma unroll
+                for (int u = 0; u < U; ++u) {
+                    const int c = c0 + u * kThreads * 4;
+                    t[u] = (b < A.n && c < cols) ? *(const float4 *)(xb + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+                }
+#pragma unroll
+                for (int u = 0; u < U; ++u) {
+                    const int c = c0 + u * kThreads * 4;
+                    if (c < ld) {
+                        *(float4 *)(xs + b * ld + xidx<E, CW>(c)) = t[u];
+                        if (NORM)
+                            ss += (double)t[u].x * t[u].x + (double)t[u].y * t[u].y + (double)t[u].z * t[u].z +
+                                  (double)t[u].w * t[u].w;
+                    }
+                }
+            }
+        } else {
+            for (int c = tid; c < ld; c += kThreads) {
+                float v = (b < A.n && c < cols) ? xb[c] : 0.0f;
+                xs[b * ld + xidx<E, CW>(c)] = v;
+                ss += (double)v * (double)v;
+            }
         }
-        if (A.norm_w) {
+        if (NORM) {
             ss = wave_sum_d(ss);
             if (lane == 0) sm.ss[b][wave] = ss;
         }
     }
     __syncthreads();
-    if (A.norm_w) {
+    if (NORM) {
         if (tid < NB) {
             double ss = 0.0;
             for (int w = 0; w < kWaves; ++w) ss += sm.ss[tid][w];
@@ -165,12 +186,12 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const GemvArgs A) {
     }
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
-        const float a = A.norm_w ? sm.a[b] : 1.0f;
+        const float a = NORM ? sm.a[b] : 1.0f;
         int wide = 0;
         for (int c = tid; c < cols; c += kThreads) {
             const int i = b * ld + xidx<E, CW>(c);
             float v = xs[i];
-            if (A.norm_w) {
+            if (NORM) {
                 v = __fmul_rn(__fmul_rn(v, a), A.norm_w[c]);  // (x*a)*w, M:6191
                 xs[i] = v;
             }
@@ -182,6 +203,21 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const GemvArgs A) {
         }
     }
     __syncthreads();
+}
+
+template <int FMT, bool FAST, int NB, int EPI, bool NORM>
+__global__ __launch_bounds__(kThreads) void gemv_kernel(const GemvArgs A) {
+    using L = Lay<FMT, FAST>;
+    constexpr int E = L::E, CW = L::CW;
+    extern __shared__ float xs[];
+    __shared__ Smem sm;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int64_t cols = A.cols;
+    const int nch = (int)((cols + CW - 1) / CW);
+    const int ld = nch * CW;  // LDS words per activation row
+
+    stage_x<E, CW, NB, NORM>(A, xs, sm, ld);
 
     // ---- row groups ------------------------------------------------------
     const int64_t rows = A.rows;
@@ -408,16 +444,334 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const GemvArgs A) {
     }
 }
 
-template <int FMT, bool FAST, int NB, int EPI>
+
+
+// ---------------------------------------------------------------------------
+// Streaming GEMV (fast layouts).  The output rows are cut into "units" (one
+// row; a gate/up or RoPE row pair for those epilogues) dealt round-robin to
+// the waves.  A wave walks the steps (unit, chunk) of its units in order, keeping the loads of the next P steps in flight
+// (16 loads of 16 B per lane) while it converts and accumulates the current
+// step; cursors advance without divisions.
+// ---------------------------------------------------------------------------
+
+// Wave sum by DPP (quad swaps, half-row and row mirrors, then the GFX9 row
+// broadcasts); fixed order, so every call gives the same bits.  The total
+// is read from lane 63 and returned uniform.
+__device__ __forceinline__ float dpp_sum(float v) {
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false));
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, false));
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xF, 0xF, false));
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x142, 0xA, 0xF, false));
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x143, 0xC, 0xF, false));
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+// Every unit is two rows: two independent 16-byte loads per lane per step
+// keep more bytes in flight per wave than one row with twice the steps.
+constexpr int kUnitRows = 2;
+
+template <int EPI>
+__host__ __device__ __forceinline__ int64_t unit_count(const GemvArgs &A) {
+    if (EPI == EPI_SWIGLU) return A.rows / 2;
+    if (EPI == EPI_ROPE_KV) return (int64_t)(A.dim + 2 * A.kvdim) / 2;
+    return (A.rows + 1) / 2;
+}
+
+// Rows of unit u: gate/up (u, H+u); RoPE pairs (j, j+half) of q and k
+// heads, then consecutive V row pairs; plain rows (2u, 2u+1), where an odd
+// last unit repeats row 2u and writes it once.
+template <int EPI>
+__device__ __forceinline__ void unit_rows(const GemvArgs &A, int64_t u, int64_t (&r)[kUnitRows]) {
+    if constexpr (EPI == EPI_SWIGLU) {
+        r[0] = u;
+        r[1] = A.rows / 2 + u;
+    } else if constexpr (EPI == EPI_ROPE_KV) {
+        const int64_t qk = (int64_t)(A.dim + A.kvdim) / 2;
+        if (u < qk) {
+            const int half = A.head_dim / 2;
+            const int64_t h = u / half;
+            r[0] = h * A.head_dim + (u - h * half);
+            r[1] = r[0] + half;
+        } else {
+            r[0] = (int64_t)A.dim + A.kvdim + 2 * (u - qk);
+            r[1] = r[0] + 1;
+        }
+    } else {
+        r[0] = 2 * u;
+        r[1] = 2 * u + 1 < A.rows ? 2 * u + 1 : 2 * u;
+    }
+}
+
+template <int FMT, int NB, int EPI, bool NORM>
+__global__ __launch_bounds__(kThreads) void gemv_stream_kernel(const GemvArgs A) {
+    using L = Lay<FMT, true>;
+    constexpr int E = L::E, CW = L::CW, R = kUnitRows;
+    // Steps in flight: 16 row loads per lane (8 when 4+ activation rows
+    // share each step and registers go to their accumulators).
+    constexpr int P = (NB <= 2 ? 16 : 8) / R;
+    extern __shared__ float xs[];
+    __shared__ Smem sm;
+    // The wave index is uniform: make it scalar so the step loop and its
+    // branches are scalar control flow.
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int64_t cols = A.cols;
+    const int nch = (int)((cols + CW - 1) / CW);
+    const int ld = nch * CW;
+
+    const int64_t rb = row_bytes(FMT, cols), sgroups = groups_of(cols);
+    const int64_t U = unit_count<EPI>(A);
+    // Units are dealt round-robin (u = wid + k*nwaves): at any moment the
+    // waves together sweep one contiguous band of rows, which spreads the
+    // traffic over every HBM channel.
+    const int64_t nwaves = (int64_t)gridDim.x * kWaves, wid = (int64_t)blockIdx.x * kWaves + wave;
+    const int64_t myunits = wid < U ? (U - 1 - wid) / nwaves + 1 : 0;
+    const int64_t steps = myunits * nch;
+    const int64_t ulast = wid + (myunits - 1) * nwaves;
+    const uint8_t *W = (const uint8_t *)A.values;
+    // Every chunk is 1 KiB of a row (Q8: 1024 codes, Q4: 2048 nibbles, F32:
+    // 256 floats) and a lane reads its 16 bytes of it.  A lane past the row
+    // end re-reads the row's first bytes: it meets zero activations (LDS is
+    // zero past cols), so its finite weights contribute exactly nothing.
+    constexpr int SPC = FMT == SRQ_Q8 ? 16 : FMT == SRQ_Q4 ? 32 : 0;  // scales per chunk
+    const int lane_sc = FMT == SRQ_Q8 ? lane / 4 : FMT == SRQ_Q4 ? lane / 2 : 0;
+
+    // Load cursor (unit lu, chunk lch) with its rows' base pointers.  Loads
+    // are unconditional straight-line code, so the compiler waits for exactly
+    // the oldest step; past the last step the cursor stays and re-reads it.
+    int64_t lu = wid;
+    int lch = 0;
+    const uint8_t *lw[R];
+    const float *ls[R];
+    auto set_rows = [&](int64_t u) {
+        int64_t r[R];
+        unit_rows<EPI>(A, u, r);
+#pragma unroll
+        for (int i = 0; i < R; ++i) {
+            lw[i] = W + r[i] * rb;
+            ls[i] = FMT == SRQ_F32 ? nullptr : A.scales + r[i] * sgroups;
+        }
+    };
+    uint4 wb[P][R];
+    float sb[P][R];
+    auto load_next = [&](uint4(&w)[R], float(&sc)[R]) {
+        const bool ok = (int64_t)lch * CW + (int64_t)lane * E < cols;
+        const int boff = ok ? lch * 1024 + lane * 16 : 0;
+        const int soff = ok ? lch * SPC + lane_sc : 0;
+#pragma unroll
+        for (int i = 0; i < R; ++i) {
+            w[i] = ld_stream16(lw[i] + boff);
+            if constexpr (FMT != SRQ_F32)
+                sc[i] = ls[i][soff];
+            else
+                sc[i] = 1.0f;
+        }
+        if (lch + 1 < nch) {
+            ++lch;
+        } else if (lu < ulast) {
+            lu += nwaves;
+            lch = 0;
+            set_rows(lu);
+        }
+    };
+    if (steps > 0) {
+        set_rows(wid);
+        // Weight loads do not depend on x: start them before staging it.
+#pragma unroll
+        for (int p = 0; p < P; ++p) load_next(wb[p], sb[p]);
+    }
+    stage_x<E, CW, NB, NORM>(A, xs, sm, ld);
+    if (steps == 0) return;  // wave-uniform; no barrier follows
+
+    float acc[R][NB];
+#pragma unroll
+    for (int i = 0; i < R; ++i)
+#pragma unroll
+        for (int b = 0; b < NB; ++b) acc[i][b] = 0.0f;
+
+    int64_t cu = wid;  // compute cursor
+    int ch = 0;
+    for (int64_t base = 0; base < steps; base += P) {
+#pragma unroll
+        for (int k = 0; k < P; ++k) {
+            const bool live = base + k < steps;  // wave-uniform
+            if (live) {
+                float xv[NB][E];
+#pragma unroll
+                for (int b = 0; b < NB; ++b) {
+                    const float *xb = xs + b * ld + ch * CW + lane * 4;
+#pragma unroll
+                    for (int q = 0; q < E / 4; ++q) {
+                        const float4 t = *(const float4 *)(xb + q * 256);
+                        xv[b][4 * q] = t.x, xv[b][4 * q + 1] = t.y, xv[b][4 * q + 2] = t.z, xv[b][4 * q + 3] = t.w;
+                    }
+                }
+#pragma unroll
+                for (int i = 0; i < R; ++i) {
+                    float wv[E];
+                    decode16<FMT>(wb[k][i], wv);
+#pragma unroll
+                    for (int b = 0; b < NB; ++b) {
+                        float p = 0.0f;
+#pragma unroll
+                        for (int e = 0; e < E; ++e) p = __builtin_fmaf(xv[b][e], wv[e], p);
+                        if constexpr (FMT == SRQ_Q4) p *= 0.0625f;  // exact: undo the *16 decode
+                        acc[i][b] = __builtin_fmaf(p, sb[k][i], acc[i][b]);
+                    }
+                }
+            }
+            load_next(wb[k], sb[k]);
+            if (!live) continue;
+            const bool done = ch == nch - 1;
+            const int64_t udone = cu;
+            if (done) {
+                ch = 0;
+                cu += nwaves;
+            } else {
+                ++ch;
+            }
+            if (!done) continue;
+
+            // ---- unit complete: reduce, FP64 fix-up, epilogue ---------------
+            int64_t r[R];
+            unit_rows<EPI>(A, udone, r);
+            float v[R][NB];
+#pragma unroll
+            for (int i = 0; i < R; ++i)
+#pragma unroll
+                for (int b = 0; b < NB; ++b) {
+                    v[i][b] = dpp_sum(acc[i][b]);
+                    acc[i][b] = 0.0f;
+                }
+            if (sm.any_wide) {
+#pragma unroll
+                for (int b = 0; b < NB; ++b) {
+                    if (!sm.wide[b]) continue;
+#pragma unroll
+                    for (int i = 0; i < R; ++i) {
+                        const uint8_t *wr = W + r[i] * rb;
+                        double d = 0.0;
+                        for (int64_t c = lane * 4; c < cols; c += 256) {
+                            double pp = 0.0;
+                            for (int e = 0; e < 4 && c + e < cols; ++e)
+                                pp += (double)xs[b * ld + xidx<E, CW>((int)(c + e))] * (double)weight_at<FMT>(wr, c + e);
+                            d += pp * (FMT == SRQ_F32 ? 1.0 : (double)A.scales[r[i] * sgroups + c / kBlock]);
+                        }
+                        v[i][b] = (float)wave_sum_d(d);
+                    }
+                }
+            }
+            if (lane < NB && lane < A.n) {
+                // Lane b writes batch row b (values are wave-uniform).
+                const int b = lane;
+                float vv[R];
+#pragma unroll
+                for (int i = 0; i < R; ++i) {
+                    vv[i] = v[i][0];
+#pragma unroll
+                    for (int bb = 1; bb < NB; ++bb)
+                        if (b == bb) vv[i] = v[i][bb];
+                }
+                float *yb = A.y + (int64_t)b * A.y_stride;
+                if constexpr (EPI == EPI_PLAIN) {
+                    yb[r[0]] = vv[0];
+                    if (r[1] != r[0]) yb[r[1]] = vv[1];
+                } else if constexpr (EPI == EPI_RESID) {
+                    const float *rb0 = A.residual + (int64_t)b * A.y_stride;
+                    yb[r[0]] = rb0[r[0]] + vv[0];
+                    if (r[1] != r[0]) yb[r[1]] = rb0[r[1]] + vv[1];
+                } else if constexpr (EPI == EPI_SWIGLU) {
+                    // h = f32(g / (1 + exp(-g))) * u  (M:6411-6413)
+                    const double gd = (double)vv[0];
+                    const float sg = (float)(gd / (1.0 + exp(-gd)));
+                    yb[r[0]] = __fmul_rn(sg, vv[1]);
+                } else {  // EPI_ROPE_KV
+                    float a = vv[0], z = vv[1];
+                    if (A.bias) {
+                        a = __fadd_rn(a, A.bias[r[0]]);
+                        z = __fadd_rn(z, A.bias[r[1]]);
+                    }
+                    const int row = A.row0 + b;
+                    const int pos = A.meta.pos[row];
+                    const int64_t qk_rows = (int64_t)A.dim + A.kvdim;
+                    if (r[0] < qk_rows) {
+                        const int half = A.head_dim / 2;
+                        const int j = (int)(r[0] % A.head_dim);
+                        const float c = A.cos_t[(int64_t)pos * half + j];
+                        const float sn = A.sin_t[(int64_t)pos * half + j];
+                        // x' = a*c - z*s ; z' = a*s + z*c  (M:5283-5285), unfused
+                        const float na = __fsub_rn(__fmul_rn(a, c), __fmul_rn(z, sn));
+                        const float nz = __fadd_rn(__fmul_rn(a, sn), __fmul_rn(z, c));
+                        a = na;
+                        z = nz;
+                    }
+                    if (r[0] < A.dim) {
+                        yb[r[0]] = a;
+                        yb[r[1]] = z;
+                    } else {
+                        const int sess = A.meta.sess[row];
+                        const int page = A.meta.pages[(int64_t)sess * A.meta.pt_stride + pos / kPageTokens];
+                        float *kv = A.meta.kv_pool + (int64_t)page * A.meta.page_elems +
+                                    (int64_t)A.meta.layer * 2 * kPageTokens * A.kvdim +
+                                    (int64_t)(pos % kPageTokens) * A.kvdim;
+                        if (r[0] < qk_rows) {
+                            kv[r[0] - A.dim] = a;
+                            kv[r[1] - A.dim] = z;
+                        } else {
+                            float *vv2 = kv + (int64_t)kPageTokens * A.kvdim;
+                            vv2[r[0] - qk_rows] = a;
+                            vv2[r[1] - qk_rows] = z;
+                        }
+                    }
+                }
+            }
+        }
+    }
+}
+
+// Host-side launch parameters.
+int g_cus = 0;
+int device_cus() {
+    if (g_cus <= 0) {
+        int dev = 0, n = 0;
+        if (hipGetDevice(&dev) == hipSuccess &&
+            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0)
+            g_cus = n;
+        else
+            g_cus = 256;
+    }
+    return g_cus;
+}
+
+// Workgroups per CU of the streaming GEMV (tunable with SRQ_GEMV_WG_PER_CU).
+int gemv_wg_per_cu() {
+    static int v = [] {
+        const char *e = getenv("SRQ_GEMV_WG_PER_CU");
+        int x = e ? atoi(e) : 0;
+        return x > 0 && x <= 16 ? x : 2;
+    }();
+    return v;
+}
+
+template <int FMT, bool FAST, int NB, int EPI, bool NORM>
 int launch_t(hipStream_t s, const GemvArgs &a) {
     using L = Lay<FMT, FAST>;
     const int nch = (int)((a.cols + L::CW - 1) / L::CW);
     const size_t lds = (size_t)NB * nch * L::CW * sizeof(float);
     if (lds > 150 * 1024) return fail(SRQ_EINVAL, "gemv: activation rows do not fit LDS (n=%d cols=%lld)", NB, (long long)a.cols);
-    auto kern = gemv_kernel<FMT, FAST, NB, EPI>;
+    if constexpr (FAST) {
+        const int64_t units = unit_count<EPI>(a);
+        int64_t blocks = (units + kWaves - 1) / kWaves;
+        const int64_t cap = (int64_t)device_cus() * gemv_wg_per_cu();
+        if (blocks > cap) blocks = cap;
+        if (blocks < 1) blocks = 1;
+        gemv_stream_kernel<FMT, NB, EPI, NORM><<<(unsigned)blocks, kThreads, lds, s>>>(a);
+        SRQ_HIP(hipGetLastError());
+        return SRQ_OK;
+    }
+    auto kern = gemv_kernel<FMT, FAST, NB, EPI, NORM>;
     int64_t ngroups = EPI == EPI_SWIGLU ? a.rows / 2 : (a.rows + 1) / 2;
     int64_t blocks = (ngroups + kWaves - 1) / kWaves;
-    // Enough waves to keep ~8 per CU busy; each wave then loops over groups.
     const int per_cu = lds > 72 * 1024 ? 1 : lds > 48 * 1024 ? 2 : 4;
     const int64_t cap = 256LL * per_cu * 2;
     if (blocks > cap) blocks = cap;
@@ -427,41 +781,64 @@ int launch_t(hipStream_t s, const GemvArgs &a) {
     return SRQ_OK;
 }
 
-template <int FMT, bool FAST, int EPI>
+template <int FMT, bool FAST, int EPI, bool NORM>
 int launch_nb(hipStream_t s, const GemvArgs &a) {
-    if (a.n <= 1) return launch_t<FMT, FAST, 1, EPI>(s, a);
-    if (a.n <= 2) return launch_t<FMT, FAST, 2, EPI>(s, a);
-    if (a.n <= 4) return launch_t<FMT, FAST, 4, EPI>(s, a);
-    return launch_t<FMT, FAST, 8, EPI>(s, a);
+    if (a.n <= 1) return launch_t<FMT, FAST, 1, EPI, NORM>(s, a);
+    if (a.n <= 2) return launch_t<FMT, FAST, 2, EPI, NORM>(s, a);
+    if (a.n <= 4) return launch_t<FMT, FAST, 4, EPI, NORM>(s, a);
+    return launch_t<FMT, FAST, 8, EPI, NORM>(s, a);
 }
 
+// Instantiated variants: plain (linear), plain + norm (head), residual
+// (o, down), norm + SwiGLU (gate/up), norm + RoPE/KV (q/k/v).
 template <int FMT, bool FAST>
 int launch_epi(hipStream_t s, const GemvArgs &a) {
+    const bool norm = a.norm_w != nullptr;
     switch (a.epilogue) {
-        case EPI_PLAIN: return launch_nb<FMT, FAST, EPI_PLAIN>(s, a);
-        case EPI_RESID: return launch_nb<FMT, FAST, EPI_RESID>(s, a);
-        case EPI_SWIGLU: return launch_nb<FMT, FAST, EPI_SWIGLU>(s, a);
-        case EPI_ROPE_KV: return launch_nb<FMT, FAST, EPI_ROPE_KV>(s, a);
+        case EPI_PLAIN:
+            return norm ? launch_nb<FMT, FAST, EPI_PLAIN, true>(s, a) : launch_nb<FMT, FAST, EPI_PLAIN, false>(s, a);
+        case EPI_RESID:
+            if (norm) break;
+            return launch_nb<FMT, FAST, EPI_RESID, false>(s, a);
+        case EPI_SWIGLU:
+            if (!norm) break;
+            return launch_nb<FMT, FAST, EPI_SWIGLU, true>(s, a);
+        case EPI_ROPE_KV:
+            if (!norm) break;
+            return launch_nb<FMT, FAST, EPI_ROPE_KV, true>(s, a);
     }
-    return fail(SRQ_EINVAL, "gemv: bad epilogue");
+    return fail(SRQ_EINVAL, "gemv: unsupported epilogue/norm combination");
 }
 
-template <int FMT, bool FAST, int EPI>
+template <int FMT, bool FAST, int EPI, bool NORM>
 hipError_t prepare_nb() {
-    const void *fns[] = {(const void *)gemv_kernel<FMT, FAST, 1, EPI>, (const void *)gemv_kernel<FMT, FAST, 2, EPI>,
-                         (const void *)gemv_kernel<FMT, FAST, 4, EPI>, (const void *)gemv_kernel<FMT, FAST, 8, EPI>};
+    const void *fns[] = {(const void *)gemv_kernel<FMT, FAST, 1, EPI, NORM>,
+                         (const void *)gemv_kernel<FMT, FAST, 2, EPI, NORM>,
+                         (const void *)gemv_kernel<FMT, FAST, 4, EPI, NORM>,
+                         (const void *)gemv_kernel<FMT, FAST, 8, EPI, NORM>};
     hipError_t err = hipSuccess;
     for (const void *f : fns) {
         hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, 150 * 1024);
         if (e != hipSuccess) err = e;
+    }
+    if constexpr (FAST) {
+        const void *sf[] = {(const void *)gemv_stream_kernel<FMT, 1, EPI, NORM>,
+                            (const void *)gemv_stream_kernel<FMT, 2, EPI, NORM>,
+                            (const void *)gemv_stream_kernel<FMT, 4, EPI, NORM>,
+                            (const void *)gemv_stream_kernel<FMT, 8, EPI, NORM>};
+        for (const void *f : sf) {
+            hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, 150 * 1024);
+            if (e != hipSuccess) err = e;
+        }
     }
     return err;
 }
 
 template <int FMT, bool FAST>
 hipError_t prepare_epi() {
-    hipError_t e[4] = {prepare_nb<FMT, FAST, EPI_PLAIN>(), prepare_nb<FMT, FAST, EPI_RESID>(),
-                       prepare_nb<FMT, FAST, EPI_SWIGLU>(), prepare_nb<FMT, FAST, EPI_ROPE_KV>()};
+    hipError_t e[5] = {prepare_nb<FMT, FAST, EPI_PLAIN, false>(), prepare_nb<FMT, FAST, EPI_PLAIN, true>(),
+                       prepare_nb<FMT, FAST, EPI_RESID, false>(), prepare_nb<FMT, FAST, EPI_SWIGLU, true>(),
+                       prepare_nb<FMT, FAST, EPI_ROPE_KV, true>()};
     for (hipError_t x : e)
         if (x != hipSuccess) return x;
     return hipSuccess;
@@ -486,7 +863,9 @@ int gemv_max_rows(int fmt, int64_t cols) {
     const bool fast = gemv_fast_ok(fmt, cols);
     const int64_t cw = !fast ? 256 : fmt == SRQ_Q8 ? 1024 : fmt == SRQ_Q4 ? 2048 : 256;
     const int64_t ld = (cols + cw - 1) / cw * cw;
-    for (int nb = 8; nb >= 1; nb /= 2)
+    // Fast layouts stream with at most 4 rows per launch (8 would spill
+    // registers); larger batches are chunked by the caller.
+    for (int nb = fast ? 4 : 8; nb >= 1; nb /= 2)
         if (nb * ld * 4 <= 150 * 1024) return nb;
     return 0;
 }

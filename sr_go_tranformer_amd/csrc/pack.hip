@@ -121,7 +121,37 @@ __global__ __launch_bounds__(256) void dequant_kernel(int64_t cols, const void *
     }
 }
 
+// SplitMix64 output number k (k >= 1) from state `seed` (M:1416-1422):
+// the state after k calls is seed + k*gamma, so draws are independent.
+__device__ inline uint64_t splitmix_at(uint64_t seed, uint64_t k) {
+    uint64_t z = seed + k * 0x9e3779b97f4a7c15ULL;
+    z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ULL;
+    z = (z ^ (z >> 27)) * 0x94d049bb133111ebULL;
+    return z ^ (z >> 31);
+}
+
+// dst[i] = f32(Normal() * scale) where Normal uses draws 2i+1 and 2i+2
+// (RNG.Normal M:1437-1439, random init M:5218).
+__global__ __launch_bounds__(256) void fill_normal_kernel(float *__restrict__ dst, int64_t count, uint64_t seed,
+                                                          double scale) {
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < count; i += (int64_t)gridDim.x * 256) {
+        const double u1 = (double)(splitmix_at(seed, 2 * (uint64_t)i + 1) >> 11) * (1.0 / 9007199254740992.0);
+        const double u2 = (double)(splitmix_at(seed, 2 * (uint64_t)i + 2) >> 11) * (1.0 / 9007199254740992.0);
+        const double nrm = sqrt(-2.0 * log(1.0 - u1)) * cos(2.0 * M_PI * u2);
+        dst[i] = (float)(nrm * scale);
+    }
+}
+
 }  // namespace
+
+int launch_fill_normal(hipStream_t s, float *dst, int64_t count, uint64_t seed, double scale) {
+    if (count <= 0) return SRQ_OK;
+    int64_t blocks = (count + 255) / 256;
+    if (blocks > 65536) blocks = 65536;
+    fill_normal_kernel<<<(unsigned)blocks, 256, 0, s>>>(dst, count, seed, scale);
+    SRQ_HIP(hipGetLastError());
+    return SRQ_OK;
+}
 
 int launch_pack(hipStream_t s, int fmt, int64_t rows, int64_t cols, const void *src, int dtype, void *values,
                 float *scales, int *err_flag) {

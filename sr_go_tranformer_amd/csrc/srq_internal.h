@@ -56,6 +56,7 @@ int launch_pack(hipStream_t s, int fmt, int64_t rows, int64_t cols, const void *
 int launch_convert_f32(hipStream_t s, int64_t count, const void *src, int dtype, float *dst, int *err_flag);
 int launch_dequant_rows(hipStream_t s, int fmt, int64_t cols, const void *values, const float *scales,
                         const int32_t *rows, int32_t count, float *dst);
+int launch_fill_normal(hipStream_t s, float *dst, int64_t count, uint64_t seed, double scale);
 
 // ------------------------------------------------------------------ GEMV
 enum Epilogue { EPI_PLAIN = 0, EPI_RESID = 1, EPI_SWIGLU = 2, EPI_ROPE_KV = 3 };
@@ -135,7 +136,9 @@ struct AttnArgs {
     int32_t max_len;    // upper bound of pos+1 over rows (sizes LDS)
     RowMeta meta;
 };
-int launch_attention(hipStream_t s, const AttnArgs &a);
+// scratch: attention_scratch_bytes(n, heads, head_dim, max_len) bytes.
+int launch_attention(hipStream_t s, const AttnArgs &a, float *scratch);
+size_t attention_scratch_bytes(int32_t n, int32_t heads, int32_t head_dim, int32_t max_len);
 int attention_prepare();
 
 }  // namespace srq

@@ -1,0 +1,193 @@
+"""GPU parity of the batched step (prefillSelected), KV pages, selective
+heads, greedy generation and the graph-replayed decoder, through the C ABI.
+
+Bars: FP32 models match Transformers' logits and every K/V row of the
+reference's fixtures at the reference's own 2e-5 (hf_inference_test.go:74);
+quantized models match the oracle's quantized step within
+|got - want| <= 1e-4 * max(1, |want|); greedy token sequences are identical
+to the oracle's."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import oracle
+import sr_go_tranformer_amd as srq
+from tests import gpu_models, hf_fixtures
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-4
+
+
+@pytest.fixture(scope="module")
+def ex():
+    e = srq.Executor(0)
+    yield e
+    e.close()
+
+
+def near(got, want, tol=TOL, floor=1.0):
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    assert np.all(np.isfinite(got))
+    err = np.abs(got - want) / np.maximum(floor, np.abs(want))
+    assert err.max() <= tol, (float(err.max()), int(err.argmax()))
+
+
+def absnear(got, want, tol):
+    got = np.asarray(got, np.float64)
+    assert np.all(np.isfinite(got))
+    err = np.abs(got - np.asarray(want, np.float64))
+    assert err.max() <= tol, (float(err.max()), int(err.argmax()))
+
+
+@pytest.mark.parametrize("name", hf_fixtures.NAMES)
+@pytest.mark.parametrize("chunk", [1, 4, 16, 35])
+def test_fp32_step_matches_transformers(ex, name, chunk):
+    print("fixture", name, "chunk", chunk, flush=True)
+    fx = hf_fixtures.load(name)
+    m = gpu_models.load_fixture(ex, fx, "f32", use_raw=True)
+    pool = m.pool(8)
+    cache = pool.cache(4)
+    for lo in range(0, 35, chunk):
+        hi = min(lo + chunk, 35)
+        absnear(m.step([cache], [fx.ids[lo:hi]])[0], fx.logits[hi - 1], 2e-5)
+    for pos in range(35, len(fx.ids)):
+        absnear(m.step([cache], [[fx.ids[pos]]])[0], fx.logits[pos], 2e-5)
+    assert cache.pos == len(fx.ids)
+    for layer in range(fx.layers):
+        k, v = cache.read(layer, 0, len(fx.ids))
+        absnear(k, fx.k[layer], 2e-5)
+        absnear(v, fx.v[layer], 2e-5)
+
+
+@pytest.mark.parametrize("name", ["llama_f32", "llama_untied-f32", "llama3_f32", "mistral_f32", "qwen2_f32",
+                                  "mistral_bf16"])
+@pytest.mark.parametrize("fmt", ["q8", "q4", "q4-mixed"])
+def test_quantized_step_matches_oracle(ex, name, fmt):
+    print("quantized", name, fmt, flush=True)
+    fx = hf_fixtures.load(name)
+    m = gpu_models.load_fixture(ex, fx, fmt, use_raw=True)
+    om = fx.oracle_model(fmt)
+    pool = m.pool(8)
+    cache, ocache = pool.cache(4), om.new_cache()
+    lo = 0
+    for c in (33, 1, 2, 1):
+        near(m.step([cache], [fx.ids[lo:lo + c]])[0], om.step([ocache], [fx.ids[lo:lo + c]])[0])
+        lo += c
+    for layer in range(fx.layers):
+        k, v = cache.read(layer, 0, 37)
+        near(k, np.stack([ocache.row(layer, p, 0) for p in range(37)]))
+        near(v, np.stack([ocache.row(layer, p, 1) for p in range(37)]))
+
+
+@pytest.mark.parametrize("name", ["llama_f32", "mistral_f32", "qwen2_f32"])
+def test_ragged_sessions_and_selective_heads(ex, name):
+    fx = hf_fixtures.load(name)
+    m = gpu_models.load_fixture(ex, fx, "f32")
+    pool = m.pool(16)
+    ca, cb = pool.cache(4), pool.cache(4)
+    got = m.step([ca, cb], [fx.ids[:35], fx.ids[:4]])
+    absnear(got[0], fx.logits[34], 2e-5)
+    absnear(got[1], fx.logits[3], 2e-5)
+    got = m.step([ca, cb], [[fx.ids[35]], [fx.ids[4]]])
+    absnear(got[0], fx.logits[35], 2e-5)
+    absnear(got[1], fx.logits[4], 2e-5)
+    cc, cd = pool.cache(4), pool.cache(4)
+    sel = m.step([cc, cd], [fx.ids[:35], fx.ids[:4]], want=[False, True])
+    assert np.all(sel[0] == 0)
+    absnear(sel[1], fx.logits[3], 2e-5)
+    assert (cc.pos, cd.pos) == (35, 4)
+
+
+def test_step_validation_never_mutates(ex):
+    fx = hf_fixtures.load("llama_f32")
+    m = gpu_models.load_fixture(ex, fx, "q8")
+    pool = m.pool(6)
+    c = pool.cache(4)
+    m.step([c], [fx.ids[:3]])
+
+    def code(fn):
+        with pytest.raises(srq.SrqError) as e:
+            fn()
+        return e.value.code
+
+    assert code(lambda: m.step([c], [[fx.vocab]])) == srq.EINVAL
+    assert code(lambda: m.step([c, c], [[1], [2]])) == srq.EINVAL
+    assert code(lambda: m.step([c], [[]])) == srq.EINVAL
+    assert code(lambda: m.step([c], [list(range(1, 127))])) == srq.ERANGE
+    small = pool.cache(1)
+    assert code(lambda: m.step([small], [list(range(1, 40))])) == srq.ENOSPC
+    flag = C.c_int32(1)
+    assert code(lambda: m.step([c], [[5]], cancel=flag)) == srq.ECANCELED
+    assert code(lambda: pool.cache(2)) == srq.ENOSPC  # 4 + 1 + 2 > 6 pages
+    assert c.pos == 3 and small.pos == 0
+    out = m.step([c], [[5]])
+    assert np.all(np.isfinite(out)) and c.pos == 4
+
+
+def test_greedy_generate_and_decoder(ex):
+    fx = hf_fixtures.load("mistral_f32")
+    for fmt in ("q8", "q4-mixed"):
+        m = gpu_models.load_fixture(ex, fx, fmt)
+        om = fx.oracle_model(fmt)
+        pool = m.pool(16)
+        ids = fx.ids[:20]
+        want, _ = oracle.greedy(om, ids, 40, 7)
+        c = pool.cache(4)
+        got = m.generate_greedy(c, ids, 40, chunk=7)
+        assert got == want, (got, want)
+        assert c.pos == 20 + 40 - 1
+        # EOS stops generation: the first produced token is the stop id.
+        c2 = pool.cache(4)
+        stop = want[5]
+        got = m.generate_greedy(c2, ids, 40, chunk=7, eos=stop)
+        k = want.index(stop) + 1
+        assert got == want[:k] and c2.pos == 20 + k - 1
+        # Decoder API: first token from the prefill argmax, then replays.
+        c3 = pool.cache(4)
+        m.step([c3], [ids])
+        first = int(m.argmax_last()[0])
+        assert first == want[0]
+        d = srq.Decoder(m, c3, first, 30)
+        d.run(10)
+        d.run(20)
+        assert d.tokens() == want[1:31] and c3.pos == 50
+        d.close()
+        c4 = pool.cache(4)
+        m.step([c4], [ids])
+        d = srq.Decoder(m, c4, first, 12, eager=True)
+        d.run(12)
+        assert d.tokens() == want[1:13] and c4.pos == 32
+        d.close()
+
+
+def test_smollm2_shape_greedy_identity(ex):
+    """SmolLM2-135M architecture (576 / 30 layers / 9:3 heads / 1536 /
+    49152 tied), seeded N(0, 0.02) weights, Q8; 32-token prompt (one MFMA
+    chunk) and 64 greedy tokens, identical to the oracle."""
+    cfg = srq.make_config(49152, 576, 30, 9, 3, 1536, 2048, 10000.0, 1e-5, True)
+    m, norms = gpu_models.synthetic(ex, cfg, "q8", seed=1)
+    om = gpu_models.oracle_from_device(ex, m, cfg, norms)
+    r = oracle.RNG(99)
+    ids = [r.intn(cfg.vocab) for _ in range(32)]
+    want, wlog = oracle.greedy(om, ids, 64, 32)
+    margins = [float(np.sort(l)[-1] - np.sort(l)[-2]) for l in wlog]
+    print("min top-2 margin %.3g" % min(margins), flush=True)
+    pool = m.pool(8)
+    c = pool.cache(4)
+    got = m.generate_greedy(c, ids, 64, chunk=32)
+    assert got == want
+    # the first logits (MFMA prefill of 32 rows) within the bound
+    c2 = pool.cache(4)
+    first = m.step([c2], [ids])[0]
+    near(first, wlog[0])
+
+
+def test_fill_normal_matches_serial_rng(ex):
+    buf = ex.empty(100000 * 4)
+    srq.fill_normal(ex, buf, 100000, 12345, 0.02)
+    got = buf.to_numpy(np.float32, (100000,))
+    want = oracle.RNG(12345).fill_normal(100000, 0.02)
+    diff = got.view(np.int32).astype(np.int64) - want.view(np.int32).astype(np.int64)
+    assert np.abs(diff).max() <= 1 and (diff != 0).mean() < 1e-3
