@@ -209,7 +209,7 @@ template <int FMT, bool FAST, int NB, int EPI, bool NORM>
 __global__ __launch_bounds__(kThreads) void gemv_kernel(const GemvArgs A) {
     using L = Lay<FMT, FAST>;
     constexpr int E = L::E, CW = L::CW;
-    extern __shared__ float xs[];
+    extern __shared__ __attribute__((aligned(16))) float xs[];  // 16 B: ds_read_b128
     __shared__ Smem sm;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -472,34 +472,112 @@ __device__ __forceinline__ float dpp_sum(float v) {
 constexpr int kUnitRows = 2;
 
 template <int EPI>
-__host__ __device__ __forceinline__ int64_t unit_count(const GemvArgs &A) {
-    if (EPI == EPI_SWIGLU) return A.rows / 2;
-    if (EPI == EPI_ROPE_KV) return (int64_t)(A.dim + 2 * A.kvdim) / 2;
-    return (A.rows + 1) / 2;
+__host__ __device__ __forceinline__ int unit_count(const GemvArgs &A) {
+    if (EPI == EPI_SWIGLU) return (int)(A.rows / 2);
+    if (EPI == EPI_ROPE_KV) return (A.dim + 2 * A.kvdim) / 2;
+    return (int)((A.rows + 1) / 2);
 }
+
+// Rows of one unit.  Row indices fit in 32 bits (checked at launch).
+struct Unit {
+    int r[kUnitRows];
+    int j;  // EPI_ROPE_KV: column within the half head (q/k), -1 for v rows
+};
 
 // Rows of unit u: gate/up (u, H+u); RoPE pairs (j, j+half) of q and k
 // heads, then consecutive V row pairs; plain rows (2u, 2u+1), where an odd
 // last unit repeats row 2u and writes it once.
 template <int EPI>
-__device__ __forceinline__ void unit_rows(const GemvArgs &A, int64_t u, int64_t (&r)[kUnitRows]) {
+__device__ __forceinline__ Unit unit_rows(const GemvArgs &A, int u) {
+    Unit t;
+    t.j = -1;
     if constexpr (EPI == EPI_SWIGLU) {
-        r[0] = u;
-        r[1] = A.rows / 2 + u;
+        t.r[0] = u;
+        t.r[1] = (int)(A.rows / 2) + u;
     } else if constexpr (EPI == EPI_ROPE_KV) {
-        const int64_t qk = (int64_t)(A.dim + A.kvdim) / 2;
+        const int qk = (A.dim + A.kvdim) / 2;
         if (u < qk) {
-            const int half = A.head_dim / 2;
-            const int64_t h = u / half;
-            r[0] = h * A.head_dim + (u - h * half);
-            r[1] = r[0] + half;
+            const unsigned half = (unsigned)A.head_dim / 2;
+            const unsigned h = (unsigned)u / half;
+            t.j = u - (int)(h * half);
+            t.r[0] = (int)h * A.head_dim + t.j;
+            t.r[1] = t.r[0] + (int)half;
         } else {
-            r[0] = (int64_t)A.dim + A.kvdim + 2 * (u - qk);
-            r[1] = r[0] + 1;
+            t.r[0] = A.dim + A.kvdim + 2 * (u - qk);
+            t.r[1] = t.r[0] + 1;
         }
     } else {
-        r[0] = 2 * u;
-        r[1] = 2 * u + 1 < A.rows ? 2 * u + 1 : 2 * u;
+        t.r[0] = 2 * u;
+        t.r[1] = 2 * u + 1 < A.rows ? 2 * u + 1 : 2 * u;
+    }
+    return t;
+}
+
+// Write one unit's results: lane b (b < NB, b < n, write) stores batch
+// row b; values v[i][b] are wave-uniform.
+template <int EPI, int NB>
+__device__ __forceinline__ void unit_epilogue(const GemvArgs &A, const Unit &t, const float (&v)[kUnitRows][NB],
+                                              int lane, bool write) {
+    if (!(write && lane < NB && lane < A.n)) return;
+    const int *r = t.r;
+    const int b = lane;
+    float vv[kUnitRows];
+#pragma unroll
+    for (int i = 0; i < kUnitRows; ++i) {
+        vv[i] = v[i][0];
+#pragma unroll
+        for (int bb = 1; bb < NB; ++bb)
+            if (b == bb) vv[i] = v[i][bb];
+    }
+    float *yb = A.y + (int64_t)b * A.y_stride;
+    if constexpr (EPI == EPI_PLAIN) {
+        yb[r[0]] = vv[0];
+        if (r[1] != r[0]) yb[r[1]] = vv[1];
+    } else if constexpr (EPI == EPI_RESID) {
+        const float *rb0 = A.residual + (int64_t)b * A.y_stride;
+        yb[r[0]] = rb0[r[0]] + vv[0];
+        if (r[1] != r[0]) yb[r[1]] = rb0[r[1]] + vv[1];
+    } else if constexpr (EPI == EPI_SWIGLU) {
+        // h = f32(g / (1 + exp(-g))) * u  (M:6411-6413)
+        const double gd = (double)vv[0];
+        const float sg = (float)(gd / (1.0 + exp(-gd)));
+        yb[r[0]] = __fmul_rn(sg, vv[1]);
+    } else {  // EPI_ROPE_KV
+        float a = vv[0], z = vv[1];
+        if (A.bias) {
+            a = __fadd_rn(a, A.bias[r[0]]);
+            z = __fadd_rn(z, A.bias[r[1]]);
+        }
+        const int row = A.row0 + b;
+        const int pos = A.meta.pos[row];
+        const int qk_rows = A.dim + A.kvdim;
+        if (t.j >= 0) {
+            const int half = A.head_dim / 2;
+            const float c = A.cos_t[pos * half + t.j];
+            const float sn = A.sin_t[pos * half + t.j];
+            // x' = a*c - z*s ; z' = a*s + z*c  (M:5283-5285), unfused
+            const float na = __fsub_rn(__fmul_rn(a, c), __fmul_rn(z, sn));
+            const float nz = __fadd_rn(__fmul_rn(a, sn), __fmul_rn(z, c));
+            a = na;
+            z = nz;
+        }
+        if (r[0] < A.dim) {
+            yb[r[0]] = a;
+            yb[r[1]] = z;
+        } else {
+            const int sess = A.meta.sess[row];
+            const int page = A.meta.pages[(int64_t)sess * A.meta.pt_stride + pos / kPageTokens];
+            float *kv = A.meta.kv_pool + (int64_t)page * A.meta.page_elems +
+                        (int64_t)(A.meta.layer * 2 * kPageTokens + pos % kPageTokens) * A.kvdim;
+            if (r[0] < qk_rows) {
+                kv[r[0] - A.dim] = a;
+                kv[r[1] - A.dim] = z;
+            } else {
+                float *vrow = kv + (int64_t)kPageTokens * A.kvdim;
+                vrow[r[0] - qk_rows] = a;
+                vrow[r[1] - qk_rows] = z;
+            }
+        }
     }
 }
 
@@ -510,7 +588,7 @@ __global__ __launch_bounds__(kThreads) void gemv_stream_kernel(const GemvArgs A)
     // Steps in flight: 16 row loads per lane (8 when 4+ activation rows
     // share each step and registers go to their accumulators).
     constexpr int P = (NB <= 2 ? 16 : 8) / R;
-    extern __shared__ float xs[];
+    extern __shared__ __attribute__((aligned(16))) float xs[];  // 16 B: ds_read_b128
     __shared__ Smem sm;
     // The wave index is uniform: make it scalar so the step loop and its
     // branches are scalar control flow.
@@ -520,14 +598,14 @@ __global__ __launch_bounds__(kThreads) void gemv_stream_kernel(const GemvArgs A)
     const int ld = nch * CW;
 
     const int64_t rb = row_bytes(FMT, cols), sgroups = groups_of(cols);
-    const int64_t U = unit_count<EPI>(A);
+    const int U = unit_count<EPI>(A);
     // Units are dealt round-robin (u = wid + k*nwaves): at any moment the
     // waves together sweep one contiguous band of rows, which spreads the
     // traffic over every HBM channel.
-    const int64_t nwaves = (int64_t)gridDim.x * kWaves, wid = (int64_t)blockIdx.x * kWaves + wave;
-    const int64_t myunits = wid < U ? (U - 1 - wid) / nwaves + 1 : 0;
-    const int64_t steps = myunits * nch;
-    const int64_t ulast = wid + (myunits - 1) * nwaves;
+    const int nwaves = (int)gridDim.x * kWaves, wid = (int)blockIdx.x * kWaves + wave;
+    const int myunits = wid < U ? (U - 1 - wid) / nwaves + 1 : 0;
+    const int steps = myunits * nch;
+    const int ulast = wid + (myunits - 1) * nwaves;
     const uint8_t *W = (const uint8_t *)A.values;
     // Every chunk is 1 KiB of a row (Q8: 1024 codes, Q4: 2048 nibbles, F32:
     // 256 floats) and a lane reads its 16 bytes of it.  A lane past the row
@@ -539,17 +617,16 @@ __global__ __launch_bounds__(kThreads) void gemv_stream_kernel(const GemvArgs A)
     // Load cursor (unit lu, chunk lch) with its rows' base pointers.  Loads
     // are unconditional straight-line code, so the compiler waits for exactly
     // the oldest step; past the last step the cursor stays and re-reads it.
-    int64_t lu = wid;
+    int lu = wid;
     int lch = 0;
     const uint8_t *lw[R];
     const float *ls[R];
-    auto set_rows = [&](int64_t u) {
-        int64_t r[R];
-        unit_rows<EPI>(A, u, r);
+    auto set_rows = [&](int u) {
+        const Unit t = unit_rows<EPI>(A, u);
 #pragma unroll
         for (int i = 0; i < R; ++i) {
-            lw[i] = W + r[i] * rb;
-            ls[i] = FMT == SRQ_F32 ? nullptr : A.scales + r[i] * sgroups;
+            lw[i] = W + (uint64_t)(uint32_t)t.r[i] * (uint64_t)rb;
+            ls[i] = FMT == SRQ_F32 ? nullptr : A.scales + (uint64_t)(uint32_t)t.r[i] * (uint64_t)sgroups;
         }
     };
     uint4 wb[P][R];
@@ -582,6 +659,8 @@ __global__ __launch_bounds__(kThreads) void gemv_stream_kernel(const GemvArgs A)
     }
     stage_x<E, CW, NB, NORM>(A, xs, sm, ld);
     if (steps == 0) return;  // wave-uniform; no barrier follows
+    // Batch rows flagged wide are written by the FP64 pass below instead.
+    const bool fast_row = !(lane < NB && sm.wide[lane]);
 
     float acc[R][NB];
 #pragma unroll
@@ -589,9 +668,9 @@ __global__ __launch_bounds__(kThreads) void gemv_stream_kernel(const GemvArgs A)
 #pragma unroll
         for (int b = 0; b < NB; ++b) acc[i][b] = 0.0f;
 
-    int64_t cu = wid;  // compute cursor
+    int cu = wid;  // compute cursor
     int ch = 0;
-    for (int64_t base = 0; base < steps; base += P) {
+    for (int base = 0; base < steps; base += P) {
 #pragma unroll
         for (int k = 0; k < P; ++k) {
             const bool live = base + k < steps;  // wave-uniform
@@ -623,7 +702,7 @@ __global__ __launch_bounds__(kThreads) void gemv_stream_kernel(const GemvArgs A)
             load_next(wb[k], sb[k]);
             if (!live) continue;
             const bool done = ch == nch - 1;
-            const int64_t udone = cu;
+            const int udone = cu;
             if (done) {
                 ch = 0;
                 cu += nwaves;
@@ -632,9 +711,8 @@ __global__ __launch_bounds__(kThreads) void gemv_stream_kernel(const GemvArgs A)
             }
             if (!done) continue;
 
-            // ---- unit complete: reduce, FP64 fix-up, epilogue ---------------
-            int64_t r[R];
-            unit_rows<EPI>(A, udone, r);
+            // Unit complete: reduce and write.
+            const Unit t = unit_rows<EPI>(A, udone);
             float v[R][NB];
 #pragma unroll
             for (int i = 0; i < R; ++i)
@@ -643,89 +721,36 @@ __global__ __launch_bounds__(kThreads) void gemv_stream_kernel(const GemvArgs A)
                     v[i][b] = dpp_sum(acc[i][b]);
                     acc[i][b] = 0.0f;
                 }
-            if (sm.any_wide) {
+            unit_epilogue<EPI, NB>(A, t, v, lane, fast_row);
+        }
+    }
+
+    // FP64 pass for batch rows holding |x| > kWideLimit (M:4356-4382):
+    // Sum_g f64(scale_g) * Sum_j f64(x_j) * f64(w_j), then the epilogue.
+    if (!sm.any_wide) return;
+    for (int u = wid; u < U; u += nwaves) {
+        const Unit t = unit_rows<EPI>(A, u);
+        const int *r = t.r;
+        float v[R][NB] = {};
+        for (int b = 0; b < NB; ++b) {
+            if (!sm.wide[b]) continue;
 #pragma unroll
-                for (int b = 0; b < NB; ++b) {
-                    if (!sm.wide[b]) continue;
-#pragma unroll
-                    for (int i = 0; i < R; ++i) {
-                        const uint8_t *wr = W + r[i] * rb;
-                        double d = 0.0;
-                        for (int64_t c = lane * 4; c < cols; c += 256) {
-                            double pp = 0.0;
-                            for (int e = 0; e < 4 && c + e < cols; ++e)
-                                pp += (double)xs[b * ld + xidx<E, CW>((int)(c + e))] * (double)weight_at<FMT>(wr, c + e);
-                            d += pp * (FMT == SRQ_F32 ? 1.0 : (double)A.scales[r[i] * sgroups + c / kBlock]);
-                        }
-                        v[i][b] = (float)wave_sum_d(d);
-                    }
+            for (int i = 0; i < R; ++i) {
+                const uint8_t *wr = W + (int64_t)r[i] * rb;
+                double d = 0.0;
+                for (int64_t c = lane * 4; c < cols; c += 256) {
+                    double pp = 0.0;
+                    for (int e = 0; e < 4 && c + e < cols; ++e)
+                        pp += (double)xs[b * ld + xidx<E, CW>((int)(c + e))] * (double)weight_at<FMT>(wr, c + e);
+                    d += pp * (FMT == SRQ_F32 ? 1.0 : (double)A.scales[(int64_t)r[i] * sgroups + c / kBlock]);
                 }
-            }
-            if (lane < NB && lane < A.n) {
-                // Lane b writes batch row b (values are wave-uniform).
-                const int b = lane;
-                float vv[R];
+                const float f = (float)wave_sum_d(d);
 #pragma unroll
-                for (int i = 0; i < R; ++i) {
-                    vv[i] = v[i][0];
-#pragma unroll
-                    for (int bb = 1; bb < NB; ++bb)
-                        if (b == bb) vv[i] = v[i][bb];
-                }
-                float *yb = A.y + (int64_t)b * A.y_stride;
-                if constexpr (EPI == EPI_PLAIN) {
-                    yb[r[0]] = vv[0];
-                    if (r[1] != r[0]) yb[r[1]] = vv[1];
-                } else if constexpr (EPI == EPI_RESID) {
-                    const float *rb0 = A.residual + (int64_t)b * A.y_stride;
-                    yb[r[0]] = rb0[r[0]] + vv[0];
-                    if (r[1] != r[0]) yb[r[1]] = rb0[r[1]] + vv[1];
-                } else if constexpr (EPI == EPI_SWIGLU) {
-                    // h = f32(g / (1 + exp(-g))) * u  (M:6411-6413)
-                    const double gd = (double)vv[0];
-                    const float sg = (float)(gd / (1.0 + exp(-gd)));
-                    yb[r[0]] = __fmul_rn(sg, vv[1]);
-                } else {  // EPI_ROPE_KV
-                    float a = vv[0], z = vv[1];
-                    if (A.bias) {
-                        a = __fadd_rn(a, A.bias[r[0]]);
-                        z = __fadd_rn(z, A.bias[r[1]]);
-                    }
-                    const int row = A.row0 + b;
-                    const int pos = A.meta.pos[row];
-                    const int64_t qk_rows = (int64_t)A.dim + A.kvdim;
-                    if (r[0] < qk_rows) {
-                        const int half = A.head_dim / 2;
-                        const int j = (int)(r[0] % A.head_dim);
-                        const float c = A.cos_t[(int64_t)pos * half + j];
-                        const float sn = A.sin_t[(int64_t)pos * half + j];
-                        // x' = a*c - z*s ; z' = a*s + z*c  (M:5283-5285), unfused
-                        const float na = __fsub_rn(__fmul_rn(a, c), __fmul_rn(z, sn));
-                        const float nz = __fadd_rn(__fmul_rn(a, sn), __fmul_rn(z, c));
-                        a = na;
-                        z = nz;
-                    }
-                    if (r[0] < A.dim) {
-                        yb[r[0]] = a;
-                        yb[r[1]] = z;
-                    } else {
-                        const int sess = A.meta.sess[row];
-                        const int page = A.meta.pages[(int64_t)sess * A.meta.pt_stride + pos / kPageTokens];
-                        float *kv = A.meta.kv_pool + (int64_t)page * A.meta.page_elems +
-                                    (int64_t)A.meta.layer * 2 * kPageTokens * A.kvdim +
-                                    (int64_t)(pos % kPageTokens) * A.kvdim;
-                        if (r[0] < qk_rows) {
-                            kv[r[0] - A.dim] = a;
-                            kv[r[1] - A.dim] = z;
-                        } else {
-                            float *vv2 = kv + (int64_t)kPageTokens * A.kvdim;
-                            vv2[r[0] - qk_rows] = a;
-                            vv2[r[1] - qk_rows] = z;
-                        }
-                    }
-                }
+                for (int bb = 0; bb < NB; ++bb)
+                    if (bb == b) v[i][bb] = f;
             }
         }
+        unit_epilogue<EPI, NB>(A, t, v, lane, !fast_row);
     }
 }
 
@@ -760,11 +785,17 @@ int launch_t(hipStream_t s, const GemvArgs &a) {
     const size_t lds = (size_t)NB * nch * L::CW * sizeof(float);
     if (lds > 150 * 1024) return fail(SRQ_EINVAL, "gemv: activation rows do not fit LDS (n=%d cols=%lld)", NB, (long long)a.cols);
     if constexpr (FAST) {
+        // The kernel indexes rows, units and steps in 32 bits.
+        if (a.rows >= (1LL << 30))
+            return fail(SRQ_EINVAL, "gemv: %lld rows exceed the 2^30 row limit", (long long)a.rows);
         const int64_t units = unit_count<EPI>(a);
         int64_t blocks = (units + kWaves - 1) / kWaves;
         const int64_t cap = (int64_t)device_cus() * gemv_wg_per_cu();
         if (blocks > cap) blocks = cap;
         if (blocks < 1) blocks = 1;
+        if ((units / (blocks * kWaves) + 1) * nch >= (1LL << 31))
+            return fail(SRQ_EINVAL, "gemv: %lld x %lld exceeds the per-wave step limit", (long long)a.rows,
+                        (long long)a.cols);
         gemv_stream_kernel<FMT, NB, EPI, NORM><<<(unsigned)blocks, kThreads, lds, s>>>(a);
         SRQ_HIP(hipGetLastError());
         return SRQ_OK;
