@@ -12,9 +12,10 @@ executor's stream (bracketed by stream synchronisation).
 
 Reported:
   value          weight bytes streamed per decode token x tokens/s (GB/s)
-  roofline       the Q8 dequant-GEMV kernel at 14336 x 4096, batch 1,
-                 timed launch by launch with HIP events over the 32 distinct
-                 up-projection matrices (2 GB, far beyond the 256 MB MALL)
+  roofline       the Q8 dequant-GEMV kernel at 14336 x 4096, batch 1:
+                 back-to-back launches over the 32 distinct up-projection
+                 matrices (2 GB, far beyond the 256 MB MALL) between one
+                 pair of HIP events on the launch stream
   cpu_baseline   the oracle (C restatement of the reference's Go CPU path)
                  decoding a few tokens of the same model on the host cores
 """
@@ -67,31 +68,32 @@ class HipEvents:
         self.hip.hipEventDestroy(ev)
 
 
-def gemv_roofline(srq, ex, model, cfg, hip, launches):
-    """Time the Q8 GEMV at 14336x4096 (batch 1) launch by launch."""
-    ups = [model.weight(srq.T_UP, layer) for layer in range(cfg.layers)]
-    rows, cols = ups[0].rows, ups[0].cols
+def gemv_roofline(srq, ex, weights, hip, launches):
+    """Time the Q8 GEMV at 14336x4096 (batch 1): `launches` back-to-back
+    launches cycling over `weights` (distinct matrices, together far larger
+    than the 256 MB MALL), one HIP event pair on the launch stream around
+    all of them."""
+    rows, cols = weights[0].rows, weights[0].cols
     x = ex.empty(cols * 4)
     srq.fill_normal(ex, x, cols, 7, 1.0)
     y = ex.empty(rows * 4)
     stream = C.c_void_p(ex.stream)
     L = srq.lib()
-    for w in ups[:4]:  # warm the code path
+    for w in weights[:4]:  # warm the code path
         srq.check(L.srq_linear_enqueue(ex.h, y.ptr, x.ptr, w.h, 1))
     ex.synchronize()
-    evs = [(hip.create(), hip.create()) for _ in range(launches)]
-    for i, (a, b) in enumerate(evs):
-        hip.record(a, stream)
-        srq.check(L.srq_linear_enqueue(ex.h, y.ptr, x.ptr, ups[i % len(ups)].h, 1))
-        hip.record(b, stream)
+    a, b = hip.create(), hip.create()
+    hip.record(a, stream)
+    for i in range(launches):
+        srq.check(L.srq_linear_enqueue(ex.h, y.ptr, x.ptr, weights[i % len(weights)].h, 1))
+    hip.record(b, stream)
+    ms = hip.elapsed_ms(a, b)
     ex.synchronize()
-    ms = [hip.elapsed_ms(a, b) for a, b in evs]
-    for a, b in evs:
-        hip.destroy(a)
-        hip.destroy(b)
+    hip.destroy(a)
+    hip.destroy(b)
     vb, sb = srq.packed_bytes(srq.Q8, rows, cols)
     algo = vb + sb + cols * 4 + rows * 4
-    avg_s = float(np.mean(ms)) / 1e3
+    avg_s = ms / 1e3 / launches
     achieved = algo / avg_s / 1e9
     return {
         "kernel": "gemv_stream_kernel<Q8, n=1, plain> 14336x4096",
@@ -100,6 +102,31 @@ def gemv_roofline(srq, ex, model, cfg, hip, launches):
         "algorithmic_bytes_per_launch": algo, "avg_launch_us": round(avg_s * 1e6, 3),
         "launches": launches,
     }
+
+
+def gemv_only(srq, launches, seed):
+    """The roofline leg alone, for counter runs: 32 standalone Q8 weights
+    14336x4096 packed on the device, `launches` GEMV launches, then one
+    256 MiB device-to-device copy whose known byte count calibrates the
+    FETCH_SIZE / WRITE_SIZE counters."""
+    ex = srq.Executor(0)
+    rows, cols = 14336, 4096
+    src = ex.empty(rows * cols * 4)
+    weights = []
+    for i in range(32):
+        srq.fill_normal(ex, src, rows * cols, seed * 7919 + i, 0.02)
+        h = C.c_void_p()
+        srq.check(srq.lib().srq_weight_create(ex.h, srq.Q8, rows, cols, src.ptr, srq.SRC_F32, C.byref(h)))
+        weights.append(srq.Weight(h))
+    src.close()
+    ex.synchronize()
+    roof = gemv_roofline(srq, ex, weights, HipEvents(), launches)
+    copy_bytes = 256 << 20
+    a, b = ex.empty(copy_bytes), ex.empty(copy_bytes)
+    srq.check(srq.lib().srq_copy_d2d(ex.h, b.ptr, a.ptr, copy_bytes))
+    ex.synchronize()
+    print(json.dumps({"roofline": roof, "calibration_copy_bytes": copy_bytes}), flush=True)
+    return 0
 
 
 def read_traffic():
@@ -167,6 +194,8 @@ def main():
     ap.add_argument("--cpu-tokens", type=int, default=6, help="decode tokens of the CPU baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--gemv-launches", type=int, default=320)
+    ap.add_argument("--gemv-only", action="store_true",
+                    help="run only the GEMV roofline leg (standalone weights) and a calibration copy")
     ap.add_argument("--eager", action="store_true",
                     help="launch each decode kernel directly instead of replaying the captured graph "
                          "(for kernel tracers that cannot follow graph launches)")
@@ -181,6 +210,9 @@ def main():
 
     import sr_go_tranformer_amd as srq
     from sr_go_tranformer_amd import synthetic
+
+    if args.gemv_only:
+        return gemv_only(srq, args.gemv_launches, args.seed)
 
     t_start = time.perf_counter()
     ex = srq.Executor(0)
@@ -222,7 +254,8 @@ def main():
     pos_mid = PROMPT + args.warmup + args.steps / 2.0
     kv_bytes = 2 * pos_mid * kd * 4 * cfg.layers
 
-    roof = gemv_roofline(srq, ex, model, cfg, hip, args.gemv_launches)
+    ups = [model.weight(srq.T_UP, layer) for layer in range(cfg.layers)]
+    roof = gemv_roofline(srq, ex, ups, hip, args.gemv_launches)
     print("gemv %.1f GB/s" % roof["achieved"], file=sys.stderr, flush=True)
 
     cpu = None
