@@ -109,6 +109,34 @@ def test_dequant_rows_match_copy_row(ex):
         assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
 
 
+def _q4_pairs_closed_form():
+    """q4Pairs (M:3811-3817): [b][0] = sext(b & 15), [b][1] = sext(b >> 4)."""
+    b = np.arange(256)
+    lo, hi = b & 15, b >> 4
+    return np.stack([np.where(lo > 7, lo - 16, lo), np.where(hi > 7, hi - 16, hi)], 1).astype(np.float64)
+
+
+@pytest.mark.parametrize("n", [1, 3, 8, 40])
+def test_q4_every_byte_decodes_to_pair_table(ex, n):
+    """Every packed Q4 byte, in the GEMV (n <= 16) and MFMA GEMM (n > 16)
+    kernels and in dequant_rows, decodes to the shared pair table."""
+    print("q4 bytes", n, flush=True)
+    rows, cols = 24, 1024  # 512 bytes per row: each byte value twice per row
+    rng = np.random.default_rng(n)
+    values = np.stack([rng.permutation(np.tile(np.arange(256, dtype=np.uint8), 2)) for _ in range(rows)])
+    scales = np.ones((rows, cols // 64), np.float32)
+    scales[::3] = np.float32(0.5)  # powers of two keep every product exact
+    w = srq.Weight.wrap(ex, srq.Q4, values, scales, cols)
+    table = _q4_pairs_closed_form()
+    dense = table[values].reshape(rows, cols) * np.repeat(scales.astype(np.float64), 64, axis=1)
+    got = w.dequant_rows(ex, list(range(rows)))
+    assert np.array_equal(got.astype(np.float64), dense)
+    # x of small integers: every partial sum is an exact f32 integer
+    x = rng.integers(-3, 4, size=(n, cols)).astype(np.float32)
+    y = srq.linear(ex, w, x)
+    assert np.array_equal(y.astype(np.float64), x.astype(np.float64) @ dense.T)
+
+
 def _weights(ex, dense, fmt):
     ofmt = {srq.Q8: oracle.Q8, srq.Q4: oracle.Q4, srq.F32: oracle.F32}[fmt]
     return srq.Weight.create(ex, dense, fmt), oracle.Weight.from_dense(dense, ofmt)
