@@ -799,17 +799,17 @@ int launch_t(hipStream_t s, const GemvArgs &a) {
         gemv_stream_kernel<FMT, NB, EPI, NORM><<<(unsigned)blocks, kThreads, lds, s>>>(a);
         SRQ_HIP(hipGetLastError());
         return SRQ_OK;
+    } else {
+        int64_t ngroups = EPI == EPI_SWIGLU ? a.rows / 2 : (a.rows + 1) / 2;
+        int64_t blocks = (ngroups + kWaves - 1) / kWaves;
+        const int per_cu = lds > 72 * 1024 ? 1 : lds > 48 * 1024 ? 2 : 4;
+        const int64_t cap = 256LL * per_cu * 2;
+        if (blocks > cap) blocks = cap;
+        if (blocks < 1) blocks = 1;
+        gemv_kernel<FMT, false, NB, EPI, NORM><<<(unsigned)blocks, kThreads, lds, s>>>(a);
+        SRQ_HIP(hipGetLastError());
+        return SRQ_OK;
     }
-    auto kern = gemv_kernel<FMT, FAST, NB, EPI, NORM>;
-    int64_t ngroups = EPI == EPI_SWIGLU ? a.rows / 2 : (a.rows + 1) / 2;
-    int64_t blocks = (ngroups + kWaves - 1) / kWaves;
-    const int per_cu = lds > 72 * 1024 ? 1 : lds > 48 * 1024 ? 2 : 4;
-    const int64_t cap = 256LL * per_cu * 2;
-    if (blocks > cap) blocks = cap;
-    if (blocks < 1) blocks = 1;
-    kern<<<(unsigned)blocks, kThreads, lds, s>>>(a);
-    SRQ_HIP(hipGetLastError());
-    return SRQ_OK;
 }
 
 template <int FMT, bool FAST, int EPI, bool NORM>
@@ -843,24 +843,24 @@ int launch_epi(hipStream_t s, const GemvArgs &a) {
 
 template <int FMT, bool FAST, int EPI, bool NORM>
 hipError_t prepare_nb() {
-    const void *fns[] = {(const void *)gemv_kernel<FMT, FAST, 1, EPI, NORM>,
-                         (const void *)gemv_kernel<FMT, FAST, 2, EPI, NORM>,
-                         (const void *)gemv_kernel<FMT, FAST, 4, EPI, NORM>,
-                         (const void *)gemv_kernel<FMT, FAST, 8, EPI, NORM>};
+    // The fast layouts run only the streaming kernel, the generic one only
+    // gemv_kernel; instantiate nothing else.
+    const void *fns[4];
+    if constexpr (FAST) {
+        fns[0] = (const void *)gemv_stream_kernel<FMT, 1, EPI, NORM>;
+        fns[1] = (const void *)gemv_stream_kernel<FMT, 2, EPI, NORM>;
+        fns[2] = (const void *)gemv_stream_kernel<FMT, 4, EPI, NORM>;
+        fns[3] = (const void *)gemv_stream_kernel<FMT, 8, EPI, NORM>;
+    } else {
+        fns[0] = (const void *)gemv_kernel<FMT, false, 1, EPI, NORM>;
+        fns[1] = (const void *)gemv_kernel<FMT, false, 2, EPI, NORM>;
+        fns[2] = (const void *)gemv_kernel<FMT, false, 4, EPI, NORM>;
+        fns[3] = (const void *)gemv_kernel<FMT, false, 8, EPI, NORM>;
+    }
     hipError_t err = hipSuccess;
     for (const void *f : fns) {
         hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, 150 * 1024);
         if (e != hipSuccess) err = e;
-    }
-    if constexpr (FAST) {
-        const void *sf[] = {(const void *)gemv_stream_kernel<FMT, 1, EPI, NORM>,
-                            (const void *)gemv_stream_kernel<FMT, 2, EPI, NORM>,
-                            (const void *)gemv_stream_kernel<FMT, 4, EPI, NORM>,
-                            (const void *)gemv_stream_kernel<FMT, 8, EPI, NORM>};
-        for (const void *f : sf) {
-            hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, 150 * 1024);
-            if (e != hipSuccess) err = e;
-        }
     }
     return err;
 }
