@@ -121,9 +121,9 @@ using namespace srq;
 // M:6062-6100).  Captured graphs point into a decoder's own workspace, so a
 // later step that grows the executor's workspace cannot invalidate them.
 struct Workspace {
-    DevBuf X, N, Q, A, T, H, W2, LOG, LOGC, meta, flags, ATT;
+    DevBuf X, N, Q, A, T, H, W2, LOG, LOGC, meta, flags, ATT, PLAN;
     void release_all() {
-        for (DevBuf *b : {&X, &N, &Q, &A, &T, &H, &W2, &LOG, &LOGC, &meta, &flags, &ATT}) release(*b);
+        for (DevBuf *b : {&X, &N, &Q, &A, &T, &H, &W2, &LOG, &LOGC, &meta, &flags, &ATT, &PLAN}) release(*b);
     }
 };
 
@@ -272,6 +272,8 @@ RowMeta make_meta(srq_exec *e, srq_model *m, int layer, int32_t pt_stride, const
     r.kv_pool = pool->base;
     r.page_elems = pool->page_elems;
     r.layer = layer;
+    r.kvoff = nullptr;
+    r.rope_cs = nullptr;
     (void)m;
     return r;
 }
@@ -287,7 +289,7 @@ int run_linear(srq_exec *e, Workspace &ws, const srq_weight &w, const float *x, 
         SRQ_CHECK(launch_gemm(e->stream, g, as<int32_t>(ws.flags)));
         return launch_wide_fix(e->stream, g, as<int32_t>(ws.flags));
     }
-    const int nb = gemv_max_rows(w.fmt, w.cols);
+    const int nb = gemv_max_rows(w.fmt, w.cols, norm_w != nullptr, 0);
     if (nb < 1) return fail(SRQ_EINVAL, "input width %lld exceeds the GEMV staging limit", (long long)w.cols);
     for (int32_t r0 = 0; r0 < n; r0 += nb) {
         GemvArgs a{};
@@ -898,14 +900,28 @@ int enqueue_layers(srq_exec *e, Workspace &ws, srq_model *m, srq_pool *pool, int
     float *X = as<float>(ws.X), *N = as<float>(ws.N), *Q = as<float>(ws.Q), *A = as<float>(ws.A);
     float *Hh = as<float>(ws.H), *W2 = as<float>(ws.W2);
     const bool use_gemm = n > 16 && gemm_ok(m->L[0].qkv.fmt, d) && gemm_ok(m->L[0].down.fmt, H);
+    int64_t *kvoff = nullptr;
+    float *rope_cs = nullptr;
+    if (!use_gemm) {
+        // Row plan once per step: KV offsets and RoPE rows for the fused
+        // q/k/v epilogue (ws.PLAN is sized by ensure_workspace).
+        kvoff = as<int64_t>(ws.PLAN);
+        rope_cs = (float *)(kvoff + n);
+        RowMeta meta0 = make_meta(e, m, 0, dm.pt_stride, dm.pos, dm.sess, dm.pages, pool);
+        SRQ_CHECK(launch_row_plan(e->stream, meta0, n, (int32_t)kd, m->hd, m->cos_t, m->sin_t, kvoff, rope_cs));
+    }
+    // Batch rows per fused launch: q/k/v (norm, RoPE rows, bias) and gate/up (norm).
+    const int nbq = gemv_max_rows(m->L[0].qkv.fmt, d, true, 8 * (int64_t)m->hd + (m->L[0].bias ? d + 2 * kd : 0));
+    const int nbg = gemv_max_rows(m->L[0].gu.fmt, d, true, 0);
+    if (nbq < 1 || nbg < 1) return fail(SRQ_EINVAL, "model width %lld exceeds the GEMV staging limit", (long long)d);
     for (int l = 0; l < c.layers; ++l) {
         if (cancel && *cancel) return fail(SRQ_ECANCELED, "context canceled");
         Layer &L = m->L[l];
         RowMeta meta = make_meta(e, m, l, dm.pt_stride, dm.pos, dm.sess, dm.pages, pool);
-        const int nbd = gemv_max_rows(L.qkv.fmt, d);
-        if (nbd < 1) return fail(SRQ_EINVAL, "model width %lld exceeds the GEMV staging limit", (long long)d);
+        meta.kvoff = kvoff;
+        meta.rope_cs = rope_cs;
         if (!use_gemm) {
-            for (int32_t r0 = 0; r0 < n; r0 += nbd) {
+            for (int32_t r0 = 0; r0 < n; r0 += nbq) {
                 GemvArgs a{};
                 a.fmt = L.qkv.fmt;
                 a.values = L.qkv.values;
@@ -913,7 +929,7 @@ int enqueue_layers(srq_exec *e, Workspace &ws, srq_model *m, srq_pool *pool, int
                 a.rows = L.qkv.rows;
                 a.cols = d;
                 a.x = X + r0 * d;
-                a.n = std::min(nbd, n - r0);
+                a.n = std::min(nbq, n - r0);
                 a.row0 = r0;
                 a.norm_w = L.n1;
                 a.norm_eps = c.norm_eps;
@@ -947,7 +963,7 @@ int enqueue_layers(srq_exec *e, Workspace &ws, srq_model *m, srq_pool *pool, int
         // O projection + residual (M:6398-6400).
         SRQ_CHECK(run_linear(e, ws, L.o, A, n, X, d, nullptr, 0.0, X));
         if (!use_gemm) {
-            for (int32_t r0 = 0; r0 < n; r0 += nbd) {
+            for (int32_t r0 = 0; r0 < n; r0 += nbg) {
                 GemvArgs a{};
                 a.fmt = L.gu.fmt;
                 a.values = L.gu.values;
@@ -955,7 +971,7 @@ int enqueue_layers(srq_exec *e, Workspace &ws, srq_model *m, srq_pool *pool, int
                 a.rows = 2 * H;
                 a.cols = d;
                 a.x = X + r0 * d;
-                a.n = std::min(nbd, n - r0);
+                a.n = std::min(nbg, n - r0);
                 a.row0 = r0;
                 a.norm_w = L.n2;
                 a.norm_eps = c.norm_eps;
@@ -999,6 +1015,7 @@ int ensure_workspace(srq_exec *e, Workspace &ws, srq_model *m, int32_t n, int32_
     SRQ_CHECK(ensure(ws.LOGC, (size_t)sessions * V * 4, e->stream));
     SRQ_CHECK(ensure(ws.LOG, (size_t)sessions * V * 4, e->stream));
     SRQ_CHECK(ensure(ws.ATT, attention_scratch_bytes(n, m->c.heads, m->hd, max_len), e->stream));
+    SRQ_CHECK(ensure(ws.PLAN, (size_t)n * 8 + (size_t)n * m->hd * 4, e->stream));
     return SRQ_OK;
 }
 

@@ -467,26 +467,34 @@ __device__ __forceinline__ float dpp_sum(float v) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
-// Every unit is two rows: two independent 16-byte loads per lane per step
-// keep more bytes in flight per wave than one row with twice the steps.
-constexpr int kUnitRows = 2;
+// ------------------------------------------------------- streaming kernel
+// Eight waves per workgroup, one workgroup per CU: two waves per SIMD, so one
+// wave's convert/FMA work overlaps the other's memory waits.
+constexpr int kStreamThreads = 512;
+constexpr int kStreamWaves = kStreamThreads / 64;
+
+// Rows per unit: SwiGLU pairs (gate_u, up_u) and RoPE pairs need two rows;
+// plain and residual outputs take one row per unit.
+template <int EPI>
+constexpr int unit_rows_of() {
+    return EPI == EPI_SWIGLU || EPI == EPI_ROPE_KV ? 2 : 1;
+}
 
 template <int EPI>
 __host__ __device__ __forceinline__ int unit_count(const GemvArgs &A) {
     if (EPI == EPI_SWIGLU) return (int)(A.rows / 2);
     if (EPI == EPI_ROPE_KV) return (A.dim + 2 * A.kvdim) / 2;
-    return (int)((A.rows + 1) / 2);
+    return (int)A.rows;
 }
 
 // Rows of one unit.  Row indices fit in 32 bits (checked at launch).
 struct Unit {
-    int r[kUnitRows];
-    int j;  // EPI_ROPE_KV: column within the half head (q/k), -1 for v rows
+    int r[2];
+    int j;  // EPI_ROPE_KV: column within the half head (q/k rows), -1 for v rows
 };
 
 // Rows of unit u: gate/up (u, H+u); RoPE pairs (j, j+half) of q and k
-// heads, then consecutive V row pairs; plain rows (2u, 2u+1), where an odd
-// last unit repeats row 2u and writes it once.
+// heads, then consecutive v row pairs; plain rows u.
 template <int EPI>
 __device__ __forceinline__ Unit unit_rows(const GemvArgs &A, int u) {
     Unit t;
@@ -507,68 +515,203 @@ __device__ __forceinline__ Unit unit_rows(const GemvArgs &A, int u) {
             t.r[1] = t.r[0] + 1;
         }
     } else {
-        t.r[0] = 2 * u;
-        t.r[1] = 2 * u + 1 < A.rows ? 2 * u + 1 : 2 * u;
+        t.r[0] = u;
+        t.r[1] = u;
     }
     return t;
 }
 
+// Dynamic LDS of the streaming kernel, in floats: x rows [NB x ld], then the
+// RMSNorm weight [ld] (NORM), then per batch row its RoPE {cos, sin} pairs
+// [NB x head_dim] and the q/k/v bias [rows] (EPI_ROPE_KV).
+struct StreamLds {
+    int ld, x, norm, rope, bias, total;
+};
+template <int NB, int EPI, bool NORM>
+__host__ __device__ __forceinline__ StreamLds stream_lds(const GemvArgs &A, int ld) {
+    StreamLds L;
+    L.ld = ld;
+    L.x = 0;
+    L.norm = NB * ld;
+    L.rope = L.norm + (NORM ? ld : 0);
+    L.bias = L.rope + (EPI == EPI_ROPE_KV ? NB * A.head_dim : 0);
+    const int bias_n = EPI == EPI_ROPE_KV && A.bias ? (int)A.rows : 0;
+    L.total = L.bias + ((bias_n + 3) & ~3);
+    return L;
+}
+
+struct StreamSmem {
+    double ss[8][kStreamWaves];
+    float a[8];
+    int wide[8];
+    int any_wide;
+    int64_t kvoff[8];  // EPI_ROPE_KV: element offset of each batch row's K row (layer 0)
+};
+
+// Stage the n activation rows of x into LDS (permuted, zero past cols), the
+// norm weight, RoPE rows, KV offsets and bias; apply the fused RMSNorm
+// (a = f32(1/sqrt(Sum f64(x^2)/d + eps)), y = (x*a)*w, M:6182-6194) and flag
+// rows holding |x| > kWideLimit.  One batched pass of global loads, then
+// LDS-only work.  Every thread of the workgroup calls it; ends with a barrier.
+template <int E, int CW, int NB, int EPI, bool NORM>
+__device__ __forceinline__ void stage_stream(const GemvArgs &A, float *lds, const StreamLds &L, StreamSmem &sm) {
+    constexpr int NT = kStreamThreads, NW = kStreamWaves;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int cols = (int)A.cols, ld = L.ld;
+    float *xs = lds + L.x, *wn = lds + L.norm;
+    if (tid < NB) sm.wide[tid] = 0;
+    if (tid == 0) sm.any_wide = 0;
+    if constexpr (EPI == EPI_ROPE_KV) {
+        if (tid < NB) sm.kvoff[tid] = tid < A.n ? A.meta.kvoff[A.row0 + tid] : 0;
+        const int hd = A.head_dim;
+        for (int i = tid; i < NB * hd; i += NT) {
+            const int b = i / hd;
+            lds[L.rope + i] = b < A.n ? A.meta.rope_cs[(int64_t)(A.row0 + b) * hd + (i - b * hd)] : 0.0f;
+        }
+        if (A.bias)
+            for (int i = tid; i < (int)A.rows; i += NT) lds[L.bias + i] = A.bias[i];
+    }
+    double ss[NB];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) ss[b] = 0.0;
+    const bool vec = ((((uintptr_t)A.x) | (NORM ? (uintptr_t)A.norm_w : 0)) & 15) == 0 && (cols & 3) == 0;
+    if (vec) {
+        constexpr int U = NB >= 4 ? 1 : 4 / NB;  // float4 loads in flight per row: 4 rows' worth
+        for (int c0 = tid * 4; c0 < ld; c0 += NT * 4 * U) {
+            float4 t[NB][U], w[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int c = c0 + u * NT * 4;
+#pragma unroll
+                for (int b = 0; b < NB; ++b)
+                    t[b][u] = (b < A.n && c < cols) ? *(const float4 *)(A.x + (int64_t)b * cols + c)
+                                                    : make_float4(0.f, 0.f, 0.f, 0.f);
+                if (NORM) w[u] = c < cols ? *(const float4 *)(A.norm_w + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int c = c0 + u * NT * 4;
+                if (c >= ld) continue;
+                const int i = xidx<E, CW>(c);
+#pragma unroll
+                for (int b = 0; b < NB; ++b) {
+                    *(float4 *)(xs + b * ld + i) = t[b][u];
+                    if (NORM)
+                        ss[b] += (double)t[b][u].x * t[b][u].x + (double)t[b][u].y * t[b][u].y +
+                                 (double)t[b][u].z * t[b][u].z + (double)t[b][u].w * t[b][u].w;
+                }
+                if (NORM) *(float4 *)(wn + i) = w[u];
+            }
+        }
+    } else {
+        for (int c = tid; c < ld; c += NT) {
+            const int i = xidx<E, CW>(c);
+#pragma unroll
+            for (int b = 0; b < NB; ++b) {
+                const float v = (b < A.n && c < cols) ? A.x[(int64_t)b * cols + c] : 0.0f;
+                xs[b * ld + i] = v;
+                ss[b] += (double)v * (double)v;
+            }
+            if (NORM) wn[i] = c < cols ? A.norm_w[c] : 0.0f;
+        }
+    }
+    if (NORM) {
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            const double t = wave_sum_d(ss[b]);
+            if (lane == 0) sm.ss[b][wave] = t;
+        }
+    }
+    __syncthreads();
+    if (NORM) {
+        if (tid < NB) {
+            double t = 0.0;
+            for (int w = 0; w < NW; ++w) t += sm.ss[tid][w];
+            sm.a[tid] = (float)(1.0 / sqrt(t / (double)cols + A.norm_eps));
+        }
+        __syncthreads();
+    }
+    // LDS only: normalise ((x*a)*w, unfused) and flag wide rows.  cols is a
+    // multiple of 4 for every streaming layout.
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+        const float a = NORM ? sm.a[b] : 1.0f;
+        int wide = 0;
+        for (int c = tid * 4; c < cols; c += NT * 4) {
+            const int i = xidx<E, CW>(c);
+            float4 v = *(float4 *)(xs + b * ld + i);
+            if (NORM) {
+                const float4 w = *(const float4 *)(wn + i);
+                v.x = __fmul_rn(__fmul_rn(v.x, a), w.x);
+                v.y = __fmul_rn(__fmul_rn(v.y, a), w.y);
+                v.z = __fmul_rn(__fmul_rn(v.z, a), w.z);
+                v.w = __fmul_rn(__fmul_rn(v.w, a), w.w);
+                *(float4 *)(xs + b * ld + i) = v;
+            }
+            wide |= (int)(fabsf(v.x) > kWideLimit) | (int)(fabsf(v.y) > kWideLimit) |
+                    (int)(fabsf(v.z) > kWideLimit) | (int)(fabsf(v.w) > kWideLimit);
+        }
+        if (wide && b < A.n) {
+            sm.wide[b] = 1;
+            sm.any_wide = 1;
+        }
+    }
+    __syncthreads();
+}
+
 // Write one unit's results: lane b (b < NB, b < n, write) stores batch
-// row b; values v[i][b] are wave-uniform.
-template <int EPI, int NB>
-__device__ __forceinline__ void unit_epilogue(const GemvArgs &A, const Unit &t, const float (&v)[kUnitRows][NB],
-                                              int lane, bool write) {
+// row b; values v[i][b] are wave-uniform.  resid: lane b's residual values
+// of the unit's rows (EPI_RESID).  No global loads: operands come from LDS
+// or the load stream.
+template <int EPI, int NB, int R>
+__device__ __forceinline__ void unit_epilogue(const GemvArgs &A, const Unit &t, const float (&v)[R][NB],
+                                              const float *lds, const StreamLds &L, const StreamSmem &sm,
+                                              float resid, int lane, bool write) {
     if (!(write && lane < NB && lane < A.n)) return;
     const int *r = t.r;
     const int b = lane;
-    float vv[kUnitRows];
+    // vv[i] = v[i][b]: an OR of masked bit patterns (exactly one term is
+    // nonzero), which stays in registers (an indexed pick would go through
+    // scratch memory).
+    float vv[R];
 #pragma unroll
-    for (int i = 0; i < kUnitRows; ++i) {
-        vv[i] = v[i][0];
+    for (int i = 0; i < R; ++i) {
+        uint32_t bits = 0;
 #pragma unroll
-        for (int bb = 1; bb < NB; ++bb)
-            if (b == bb) vv[i] = v[i][bb];
+        for (int bb = 0; bb < NB; ++bb) bits |= b == bb ? __float_as_uint(v[i][bb]) : 0u;
+        vv[i] = __uint_as_float(bits);
     }
     float *yb = A.y + (int64_t)b * A.y_stride;
     if constexpr (EPI == EPI_PLAIN) {
         yb[r[0]] = vv[0];
-        if (r[1] != r[0]) yb[r[1]] = vv[1];
     } else if constexpr (EPI == EPI_RESID) {
-        const float *rb0 = A.residual + (int64_t)b * A.y_stride;
-        yb[r[0]] = rb0[r[0]] + vv[0];
-        if (r[1] != r[0]) yb[r[1]] = rb0[r[1]] + vv[1];
+        yb[r[0]] = resid + vv[0];
     } else if constexpr (EPI == EPI_SWIGLU) {
         // h = f32(g / (1 + exp(-g))) * u  (M:6411-6413)
         const double gd = (double)vv[0];
         const float sg = (float)(gd / (1.0 + exp(-gd)));
-        yb[r[0]] = __fmul_rn(sg, vv[1]);
+        yb[r[0]] = __fmul_rn(sg, vv[R - 1]);
     } else {  // EPI_ROPE_KV
-        float a = vv[0], z = vv[1];
+        float a = vv[0], z = vv[R - 1];
         if (A.bias) {
-            a = __fadd_rn(a, A.bias[r[0]]);
-            z = __fadd_rn(z, A.bias[r[1]]);
+            a = __fadd_rn(a, lds[L.bias + r[0]]);
+            z = __fadd_rn(z, lds[L.bias + r[1]]);
         }
-        const int row = A.row0 + b;
-        const int pos = A.meta.pos[row];
-        const int qk_rows = A.dim + A.kvdim;
         if (t.j >= 0) {
-            const int half = A.head_dim / 2;
-            const float c = A.cos_t[pos * half + t.j];
-            const float sn = A.sin_t[pos * half + t.j];
+            const float c = lds[L.rope + b * A.head_dim + 2 * t.j];
+            const float sn = lds[L.rope + b * A.head_dim + 2 * t.j + 1];
             // x' = a*c - z*s ; z' = a*s + z*c  (M:5283-5285), unfused
             const float na = __fsub_rn(__fmul_rn(a, c), __fmul_rn(z, sn));
             const float nz = __fadd_rn(__fmul_rn(a, sn), __fmul_rn(z, c));
             a = na;
             z = nz;
         }
+        const int qk_rows = A.dim + A.kvdim;
         if (r[0] < A.dim) {
             yb[r[0]] = a;
             yb[r[1]] = z;
         } else {
-            const int sess = A.meta.sess[row];
-            const int page = A.meta.pages[(int64_t)sess * A.meta.pt_stride + pos / kPageTokens];
-            float *kv = A.meta.kv_pool + (int64_t)page * A.meta.page_elems +
-                        (int64_t)(A.meta.layer * 2 * kPageTokens + pos % kPageTokens) * A.kvdim;
+            float *kv = A.meta.kv_pool + sm.kvoff[b] + (int64_t)A.meta.layer * 2 * kPageTokens * A.kvdim;
             if (r[0] < qk_rows) {
                 kv[r[0] - A.dim] = a;
                 kv[r[1] - A.dim] = z;
@@ -582,27 +725,28 @@ __device__ __forceinline__ void unit_epilogue(const GemvArgs &A, const Unit &t, 
 }
 
 template <int FMT, int NB, int EPI, bool NORM>
-__global__ __launch_bounds__(kThreads) void gemv_stream_kernel(const GemvArgs A) {
-    using L = Lay<FMT, true>;
-    constexpr int E = L::E, CW = L::CW, R = kUnitRows;
-    // Steps in flight: 16 row loads per lane (8 when 4+ activation rows
-    // share each step and registers go to their accumulators).
-    constexpr int P = (NB <= 2 ? 16 : 8) / R;
-    extern __shared__ __attribute__((aligned(16))) float xs[];  // 16 B: ds_read_b128
-    __shared__ Smem sm;
+__global__ __launch_bounds__(kStreamThreads) void gemv_stream_kernel(const GemvArgs A) {
+    using Ly = Lay<FMT, true>;
+    constexpr int E = Ly::E, CW = Ly::CW, R = unit_rows_of<EPI>();
+    // 8 row loads in flight per lane (two waves per SIMD, eight per CU).
+    constexpr int P = 8 / R;
+    extern __shared__ __attribute__((aligned(16))) float lds[];  // 16 B: ds_read_b128
+    __shared__ StreamSmem sm;
     // The wave index is uniform: make it scalar so the step loop and its
     // branches are scalar control flow.
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int64_t cols = A.cols;
     const int nch = (int)((cols + CW - 1) / CW);
-    const int ld = nch * CW;
+    const StreamLds L = stream_lds<NB, EPI, NORM>(A, nch * CW);
+    const int ld = L.ld;
+    float *xs = lds + L.x;
 
     const int64_t rb = row_bytes(FMT, cols), sgroups = groups_of(cols);
     const int U = unit_count<EPI>(A);
     // Units are dealt round-robin (u = wid + k*nwaves): at any moment the
     // waves together sweep one contiguous band of rows, which spreads the
     // traffic over every HBM channel.
-    const int nwaves = (int)gridDim.x * kWaves, wid = (int)blockIdx.x * kWaves + wave;
+    const int nwaves = (int)gridDim.x * kStreamWaves, wid = (int)blockIdx.x * kStreamWaves + wave;
     const int myunits = wid < U ? (U - 1 - wid) / nwaves + 1 : 0;
     const int steps = myunits * nch;
     const int ulast = wid + (myunits - 1) * nwaves;
@@ -613,6 +757,8 @@ __global__ __launch_bounds__(kThreads) void gemv_stream_kernel(const GemvArgs A)
     // zero past cols), so its finite weights contribute exactly nothing.
     constexpr int SPC = FMT == SRQ_Q8 ? 16 : FMT == SRQ_Q4 ? 32 : 0;  // scales per chunk
     const int lane_sc = FMT == SRQ_Q8 ? lane / 4 : FMT == SRQ_Q4 ? lane / 2 : 0;
+    // EPI_RESID: lane b (< n) follows batch row b's residual; others row 0.
+    const float *res_row = EPI == EPI_RESID ? A.residual + (lane < A.n ? lane : 0) * A.y_stride : nullptr;
 
     // Load cursor (unit lu, chunk lch) with its rows' base pointers.  Loads
     // are unconditional straight-line code, so the compiler waits for exactly
@@ -621,6 +767,7 @@ __global__ __launch_bounds__(kThreads) void gemv_stream_kernel(const GemvArgs A)
     int lch = 0;
     const uint8_t *lw[R];
     const float *ls[R];
+    const float *lres = nullptr;
     auto set_rows = [&](int u) {
         const Unit t = unit_rows<EPI>(A, u);
 #pragma unroll
@@ -628,10 +775,12 @@ __global__ __launch_bounds__(kThreads) void gemv_stream_kernel(const GemvArgs A)
             lw[i] = W + (uint64_t)(uint32_t)t.r[i] * (uint64_t)rb;
             ls[i] = FMT == SRQ_F32 ? nullptr : A.scales + (uint64_t)(uint32_t)t.r[i] * (uint64_t)sgroups;
         }
+        if constexpr (EPI == EPI_RESID) lres = res_row + t.r[0];
     };
     uint4 wb[P][R];
     float sb[P][R];
-    auto load_next = [&](uint4(&w)[R], float(&sc)[R]) {
+    float eb[P];  // EPI_RESID: the unit's residual value, carried with each step
+    auto load_next = [&](uint4(&w)[R], float(&sc)[R], float &e) {
         const bool ok = (int64_t)lch * CW + (int64_t)lane * E < cols;
         const int boff = ok ? lch * 1024 + lane * 16 : 0;
         const int soff = ok ? lch * SPC + lane_sc : 0;
@@ -643,6 +792,7 @@ __global__ __launch_bounds__(kThreads) void gemv_stream_kernel(const GemvArgs A)
             else
                 sc[i] = 1.0f;
         }
+        if constexpr (EPI == EPI_RESID) e = *lres;
         if (lch + 1 < nch) {
             ++lch;
         } else if (lu < ulast) {
@@ -655,9 +805,9 @@ __global__ __launch_bounds__(kThreads) void gemv_stream_kernel(const GemvArgs A)
         set_rows(wid);
         // Weight loads do not depend on x: start them before staging it.
 #pragma unroll
-        for (int p = 0; p < P; ++p) load_next(wb[p], sb[p]);
+        for (int p = 0; p < P; ++p) load_next(wb[p], sb[p], eb[p]);
     }
-    stage_x<E, CW, NB, NORM>(A, xs, sm, ld);
+    stage_stream<E, CW, NB, EPI, NORM>(A, lds, L, sm);
     if (steps == 0) return;  // wave-uniform; no barrier follows
     // Batch rows flagged wide are written by the FP64 pass below instead.
     const bool fast_row = !(lane < NB && sm.wide[lane]);
@@ -675,31 +825,30 @@ __global__ __launch_bounds__(kThreads) void gemv_stream_kernel(const GemvArgs A)
         for (int k = 0; k < P; ++k) {
             const bool live = base + k < steps;  // wave-uniform
             if (live) {
-                float xv[NB][E];
+                float wv[R][E];
+#pragma unroll
+                for (int i = 0; i < R; ++i) decode16<FMT>(wb[k][i], wv[i]);
 #pragma unroll
                 for (int b = 0; b < NB; ++b) {
+                    float xv[E];
                     const float *xb = xs + b * ld + ch * CW + lane * 4;
 #pragma unroll
                     for (int q = 0; q < E / 4; ++q) {
                         const float4 t = *(const float4 *)(xb + q * 256);
-                        xv[b][4 * q] = t.x, xv[b][4 * q + 1] = t.y, xv[b][4 * q + 2] = t.z, xv[b][4 * q + 3] = t.w;
+                        xv[4 * q] = t.x, xv[4 * q + 1] = t.y, xv[4 * q + 2] = t.z, xv[4 * q + 3] = t.w;
                     }
-                }
 #pragma unroll
-                for (int i = 0; i < R; ++i) {
-                    float wv[E];
-                    decode16<FMT>(wb[k][i], wv);
-#pragma unroll
-                    for (int b = 0; b < NB; ++b) {
+                    for (int i = 0; i < R; ++i) {
                         float p = 0.0f;
 #pragma unroll
-                        for (int e = 0; e < E; ++e) p = __builtin_fmaf(xv[b][e], wv[e], p);
+                        for (int e = 0; e < E; ++e) p = __builtin_fmaf(xv[e], wv[i][e], p);
                         if constexpr (FMT == SRQ_Q4) p *= 0.0625f;  // exact: undo the *16 decode
                         acc[i][b] = __builtin_fmaf(p, sb[k][i], acc[i][b]);
                     }
                 }
             }
-            load_next(wb[k], sb[k]);
+            const float resid = eb[k];  // this step's residual, before the slot is refilled
+            load_next(wb[k], sb[k], eb[k]);
             if (!live) continue;
             const bool done = ch == nch - 1;
             const int udone = cu;
@@ -721,7 +870,7 @@ __global__ __launch_bounds__(kThreads) void gemv_stream_kernel(const GemvArgs A)
                     v[i][b] = dpp_sum(acc[i][b]);
                     acc[i][b] = 0.0f;
                 }
-            unit_epilogue<EPI, NB>(A, t, v, lane, fast_row);
+            unit_epilogue<EPI, NB, R>(A, t, v, lds, L, sm, resid, lane, fast_row);
         }
     }
 
@@ -730,19 +879,18 @@ __global__ __launch_bounds__(kThreads) void gemv_stream_kernel(const GemvArgs A)
     if (!sm.any_wide) return;
     for (int u = wid; u < U; u += nwaves) {
         const Unit t = unit_rows<EPI>(A, u);
-        const int *r = t.r;
         float v[R][NB] = {};
         for (int b = 0; b < NB; ++b) {
             if (!sm.wide[b]) continue;
 #pragma unroll
             for (int i = 0; i < R; ++i) {
-                const uint8_t *wr = W + (int64_t)r[i] * rb;
+                const uint8_t *wr = W + (int64_t)t.r[i] * rb;
                 double d = 0.0;
                 for (int64_t c = lane * 4; c < cols; c += 256) {
                     double pp = 0.0;
                     for (int e = 0; e < 4 && c + e < cols; ++e)
                         pp += (double)xs[b * ld + xidx<E, CW>((int)(c + e))] * (double)weight_at<FMT>(wr, c + e);
-                    d += pp * (FMT == SRQ_F32 ? 1.0 : (double)A.scales[(int64_t)r[i] * sgroups + c / kBlock]);
+                    d += pp * (FMT == SRQ_F32 ? 1.0 : (double)A.scales[(int64_t)t.r[i] * sgroups + c / kBlock]);
                 }
                 const float f = (float)wave_sum_d(d);
 #pragma unroll
@@ -750,7 +898,8 @@ __global__ __launch_bounds__(kThreads) void gemv_stream_kernel(const GemvArgs A)
                     if (bb == b) v[i][bb] = f;
             }
         }
-        unit_epilogue<EPI, NB>(A, t, v, lane, !fast_row);
+        const float resid = EPI == EPI_RESID && lane < A.n ? A.residual[(int64_t)lane * A.y_stride + t.r[0]] : 0.0f;
+        unit_epilogue<EPI, NB, R>(A, t, v, lds, L, sm, resid, lane, !fast_row);
     }
 }
 
@@ -773,33 +922,39 @@ int gemv_wg_per_cu() {
     static int v = [] {
         const char *e = getenv("SRQ_GEMV_WG_PER_CU");
         int x = e ? atoi(e) : 0;
-        return x > 0 && x <= 16 ? x : 2;
+        return x > 0 && x <= 4 ? x : 1;
     }();
     return v;
 }
 
+constexpr size_t kMaxLds = 150 * 1024;
+
 template <int FMT, bool FAST, int NB, int EPI, bool NORM>
 int launch_t(hipStream_t s, const GemvArgs &a) {
-    using L = Lay<FMT, FAST>;
-    const int nch = (int)((a.cols + L::CW - 1) / L::CW);
-    const size_t lds = (size_t)NB * nch * L::CW * sizeof(float);
-    if (lds > 150 * 1024) return fail(SRQ_EINVAL, "gemv: activation rows do not fit LDS (n=%d cols=%lld)", NB, (long long)a.cols);
+    using Ly = Lay<FMT, FAST>;
+    const int nch = (int)((a.cols + Ly::CW - 1) / Ly::CW);
     if constexpr (FAST) {
         // The kernel indexes rows, units and steps in 32 bits.
         if (a.rows >= (1LL << 30))
             return fail(SRQ_EINVAL, "gemv: %lld rows exceed the 2^30 row limit", (long long)a.rows);
+        const size_t lds = (size_t)stream_lds<NB, EPI, NORM>(a, nch * Ly::CW).total * sizeof(float);
+        if (lds > kMaxLds)
+            return fail(SRQ_EINVAL, "gemv: activation rows do not fit LDS (n=%d cols=%lld)", NB, (long long)a.cols);
         const int64_t units = unit_count<EPI>(a);
-        int64_t blocks = (units + kWaves - 1) / kWaves;
+        int64_t blocks = (units + kStreamWaves - 1) / kStreamWaves;
         const int64_t cap = (int64_t)device_cus() * gemv_wg_per_cu();
         if (blocks > cap) blocks = cap;
         if (blocks < 1) blocks = 1;
-        if ((units / (blocks * kWaves) + 1) * nch >= (1LL << 31))
+        if ((units / (blocks * kStreamWaves) + 1) * nch >= (1LL << 31))
             return fail(SRQ_EINVAL, "gemv: %lld x %lld exceeds the per-wave step limit", (long long)a.rows,
                         (long long)a.cols);
-        gemv_stream_kernel<FMT, NB, EPI, NORM><<<(unsigned)blocks, kThreads, lds, s>>>(a);
+        gemv_stream_kernel<FMT, NB, EPI, NORM><<<(unsigned)blocks, kStreamThreads, lds, s>>>(a);
         SRQ_HIP(hipGetLastError());
         return SRQ_OK;
     } else {
+        const size_t lds = (size_t)NB * nch * Ly::CW * sizeof(float);
+        if (lds > kMaxLds)
+            return fail(SRQ_EINVAL, "gemv: activation rows do not fit LDS (n=%d cols=%lld)", NB, (long long)a.cols);
         int64_t ngroups = EPI == EPI_SWIGLU ? a.rows / 2 : (a.rows + 1) / 2;
         int64_t blocks = (ngroups + kWaves - 1) / kWaves;
         const int per_cu = lds > 72 * 1024 ? 1 : lds > 48 * 1024 ? 2 : 4;
@@ -812,16 +967,53 @@ int launch_t(hipStream_t s, const GemvArgs &a) {
     }
 }
 
+// Widest streaming launch: 4 batch rows (Q4: 2, whose 32 codes per lane
+// per chunk leave fewer registers); the generic kernel takes 8.
+template <int FMT, bool FAST>
+constexpr int max_nb() {
+    return !FAST ? 8 : FMT == SRQ_Q4 ? 2 : 4;
+}
+
 template <int FMT, bool FAST, int EPI, bool NORM>
 int launch_nb(hipStream_t s, const GemvArgs &a) {
+    if (a.n > max_nb<FMT, FAST>())
+        return fail(SRQ_EINVAL, "gemv: %d activation rows exceed one launch (%d)", a.n, max_nb<FMT, FAST>());
     if (a.n <= 1) return launch_t<FMT, FAST, 1, EPI, NORM>(s, a);
-    if (a.n <= 2) return launch_t<FMT, FAST, 2, EPI, NORM>(s, a);
-    if (a.n <= 4) return launch_t<FMT, FAST, 4, EPI, NORM>(s, a);
-    return launch_t<FMT, FAST, 8, EPI, NORM>(s, a);
+    if (a.n <= 2 || max_nb<FMT, FAST>() == 2) return launch_t<FMT, FAST, 2, EPI, NORM>(s, a);
+    if constexpr (max_nb<FMT, FAST>() >= 4) {
+        if (a.n <= 4 || max_nb<FMT, FAST>() == 4) return launch_t<FMT, FAST, 4, EPI, NORM>(s, a);
+    }
+    if constexpr (max_nb<FMT, FAST>() >= 8) return launch_t<FMT, FAST, 8, EPI, NORM>(s, a);
+    return fail(SRQ_EINVAL, "gemv: unsupported batch");
+}
+
+template <int FMT, bool FAST, int EPI, bool NORM, int NB>
+hipError_t prepare_one() {
+    if constexpr (NB > max_nb<FMT, FAST>()) {
+        return hipSuccess;
+    } else {
+        const void *f;
+        if constexpr (FAST)
+            f = (const void *)gemv_stream_kernel<FMT, NB, EPI, NORM>;
+        else
+            f = (const void *)gemv_kernel<FMT, false, NB, EPI, NORM>;
+        return hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMaxLds);
+    }
+}
+
+template <int FMT, bool FAST, int EPI, bool NORM>
+hipError_t prepare_nb() {
+    // The fast layouts run only the streaming kernel, the generic one only
+    // gemv_kernel; instantiate nothing else.
+    const hipError_t errs[] = {prepare_one<FMT, FAST, EPI, NORM, 1>(), prepare_one<FMT, FAST, EPI, NORM, 2>(),
+                               prepare_one<FMT, FAST, EPI, NORM, 4>(), prepare_one<FMT, FAST, EPI, NORM, 8>()};
+    for (hipError_t e : errs)
+        if (e != hipSuccess) return e;
+    return hipSuccess;
 }
 
 // Instantiated variants: plain (linear), plain + norm (head), residual
-// (o, down), norm + SwiGLU (gate/up), norm + RoPE/KV (q/k/v).
+// (o / down projections), SwiGLU + norm (gate/up), RoPE/KV + norm (q/k/v).
 template <int FMT, bool FAST>
 int launch_epi(hipStream_t s, const GemvArgs &a) {
     const bool norm = a.norm_w != nullptr;
@@ -840,31 +1032,6 @@ int launch_epi(hipStream_t s, const GemvArgs &a) {
     }
     return fail(SRQ_EINVAL, "gemv: unsupported epilogue/norm combination");
 }
-
-template <int FMT, bool FAST, int EPI, bool NORM>
-hipError_t prepare_nb() {
-    // The fast layouts run only the streaming kernel, the generic one only
-    // gemv_kernel; instantiate nothing else.
-    const void *fns[4];
-    if constexpr (FAST) {
-        fns[0] = (const void *)gemv_stream_kernel<FMT, 1, EPI, NORM>;
-        fns[1] = (const void *)gemv_stream_kernel<FMT, 2, EPI, NORM>;
-        fns[2] = (const void *)gemv_stream_kernel<FMT, 4, EPI, NORM>;
-        fns[3] = (const void *)gemv_stream_kernel<FMT, 8, EPI, NORM>;
-    } else {
-        fns[0] = (const void *)gemv_kernel<FMT, false, 1, EPI, NORM>;
-        fns[1] = (const void *)gemv_kernel<FMT, false, 2, EPI, NORM>;
-        fns[2] = (const void *)gemv_kernel<FMT, false, 4, EPI, NORM>;
-        fns[3] = (const void *)gemv_kernel<FMT, false, 8, EPI, NORM>;
-    }
-    hipError_t err = hipSuccess;
-    for (const void *f : fns) {
-        hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, 150 * 1024);
-        if (e != hipSuccess) err = e;
-    }
-    return err;
-}
-
 template <int FMT, bool FAST>
 hipError_t prepare_epi() {
     hipError_t e[5] = {prepare_nb<FMT, FAST, EPI_PLAIN, false>(), prepare_nb<FMT, FAST, EPI_PLAIN, true>(),
@@ -890,17 +1057,19 @@ int gemv_prepare() {
 
 // Largest batch (8, 4, 2 or 1) whose staged activations fit the LDS budget,
 // or 0 when even one row does not fit.
-int gemv_max_rows(int fmt, int64_t cols) {
+int gemv_max_rows(int fmt, int64_t cols, bool norm, int64_t extra_floats) {
     const bool fast = gemv_fast_ok(fmt, cols);
     const int64_t cw = !fast ? 256 : fmt == SRQ_Q8 ? 1024 : fmt == SRQ_Q4 ? 2048 : 256;
     const int64_t ld = (cols + cw - 1) / cw * cw;
-    // Fast layouts stream with at most 4 rows per launch (8 would spill
-    // registers); larger batches are chunked by the caller.
-    for (int nb = fast ? 4 : 8; nb >= 1; nb /= 2)
-        if (nb * ld * 4 <= 150 * 1024) return nb;
+    // Fast layouts stream at most 4 rows per launch (Q4: 2); larger batches
+    // are chunked by the caller.  Their LDS also holds the norm weight and
+    // the epilogue's per-row data (extra_floats bounds it).
+    for (int nb = !fast ? 8 : fmt == SRQ_Q4 ? 2 : 4; nb >= 1; nb /= 2) {
+        const int64_t floats = fast ? nb * ld + (norm ? ld : 0) + extra_floats : nb * ld;
+        if (floats * 4 <= (int64_t)kMaxLds) return nb;
+    }
     return 0;
 }
-
 bool gemv_fast_ok(int fmt, int64_t cols) {
     if (fmt == SRQ_Q8) return cols % 16 == 0;
     if (fmt == SRQ_Q4) return cols % 32 == 0;

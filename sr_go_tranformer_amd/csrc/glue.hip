@@ -146,7 +146,32 @@ __global__ void advance_kernel(int32_t *pos, const int32_t *token, int32_t *out,
     }
 }
 
+// One workgroup per row: the row's KV element offset and its RoPE row.
+__global__ void row_plan_kernel(const int32_t *pos, const int32_t *sess, const int32_t *pages, int32_t pt_stride,
+                                int64_t page_elems, int32_t kvdim, int32_t half, const float *cos_t,
+                                const float *sin_t, int64_t *kvoff, float *rope_cs) {
+    const int row = blockIdx.x;
+    const int p = pos[row];
+    if (threadIdx.x == 0) {
+        const int page = pages[(int64_t)sess[row] * pt_stride + p / kPageTokens];
+        kvoff[row] = (int64_t)page * page_elems + (int64_t)(p % kPageTokens) * kvdim;
+    }
+    for (int j = threadIdx.x; j < half; j += blockDim.x) {
+        rope_cs[((int64_t)row * half + j) * 2] = cos_t[(int64_t)p * half + j];
+        rope_cs[((int64_t)row * half + j) * 2 + 1] = sin_t[(int64_t)p * half + j];
+    }
+}
+
 }  // namespace
+
+int launch_row_plan(hipStream_t s, const RowMeta &meta, int32_t n, int32_t kvdim, int32_t head_dim,
+                    const float *cos_t, const float *sin_t, int64_t *kvoff, float *rope_cs) {
+    if (n <= 0) return SRQ_OK;
+    row_plan_kernel<<<n, 64, 0, s>>>(meta.pos, meta.sess, meta.pages, meta.pt_stride, meta.page_elems, kvdim,
+                                     head_dim / 2, cos_t, sin_t, kvoff, rope_cs);
+    SRQ_HIP(hipGetLastError());
+    return SRQ_OK;
+}
 
 int launch_rmsnorm(hipStream_t s, const float *x, const float *w, float *y, int32_t n, int32_t d, double eps) {
     if (n <= 0) return SRQ_OK;

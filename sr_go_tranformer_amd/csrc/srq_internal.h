@@ -71,6 +71,9 @@ struct RowMeta {
     float *kv_pool;            // page 0
     int64_t page_elems;        // 2*32*kvdim*layers
     int32_t layer;
+    // Row plan (launch_row_plan), used by the fused GEMV epilogue:
+    const int64_t *kvoff;      // [n] element offset of the row's K row in layer 0
+    const float *rope_cs;      // [n x head_dim] {cos, sin} of the row's position, interleaved
 };
 
 struct GemvArgs {
@@ -95,7 +98,9 @@ struct GemvArgs {
 };
 int launch_gemv(hipStream_t s, const GemvArgs &a);
 bool gemv_fast_ok(int fmt, int64_t cols);
-int gemv_max_rows(int fmt, int64_t cols);
+// Batch rows per GEMV launch for a weight of `cols` inputs; norm: fused
+// RMSNorm; extra_floats: LDS floats of the epilogue's per-launch data.
+int gemv_max_rows(int fmt, int64_t cols, bool norm, int64_t extra_floats);
 int gemv_prepare();
 
 // ------------------------------------------------------------------ GEMM
@@ -127,6 +132,10 @@ int launch_gather_rows(hipStream_t s, const float *src, int64_t d, const int32_t
 int launch_argmax(hipStream_t s, const float *logits, int32_t rows, int32_t vocab, int32_t *ids, int32_t *err);
 int launch_advance(hipStream_t s, int32_t *pos, const int32_t *token, int32_t *out, int32_t *counter,
                    int32_t *embed_ids);
+// Row plan of a step's n rows: kvoff[r] = page*page_elems + (pos%32)*kvdim
+// and rope_cs[r] = {cos, sin} pairs of pos (tables [context x head_dim/2]).
+int launch_row_plan(hipStream_t s, const RowMeta &meta, int32_t n, int32_t kvdim, int32_t head_dim,
+                    const float *cos_t, const float *sin_t, int64_t *kvoff, float *rope_cs);
 
 // ------------------------------------------------------------- attention
 struct AttnArgs {
