@@ -121,9 +121,9 @@ using namespace srq;
 // M:6062-6100).  Captured graphs point into a decoder's own workspace, so a
 // later step that grows the executor's workspace cannot invalidate them.
 struct Workspace {
-    DevBuf X, N, Q, A, T, H, W2, LOG, LOGC, meta, flags, ATT, PLAN;
+    DevBuf X, N, Q, A, T, H, W2, LOG, LOGC, meta, flags, ATT, ATTC, PLAN;
     void release_all() {
-        for (DevBuf *b : {&X, &N, &Q, &A, &T, &H, &W2, &LOG, &LOGC, &meta, &flags, &ATT, &PLAN}) release(*b);
+        for (DevBuf *b : {&X, &N, &Q, &A, &T, &H, &W2, &LOG, &LOGC, &meta, &flags, &ATT, &ATTC, &PLAN}) release(*b);
     }
 };
 
@@ -959,7 +959,7 @@ int enqueue_layers(srq_exec *e, Workspace &ws, srq_model *m, srq_pool *pool, int
         at.head_dim = m->hd;
         at.max_len = max_len;
         at.meta = meta;
-        SRQ_CHECK(launch_attention(e->stream, at, as<float>(ws.ATT)));
+        SRQ_CHECK(launch_attention(e->stream, at, as<float>(ws.ATT), as<int32_t>(ws.ATTC)));
         // O projection + residual (M:6398-6400).
         SRQ_CHECK(run_linear(e, ws, L.o, A, n, X, d, nullptr, 0.0, X));
         if (!use_gemm) {
@@ -1016,6 +1016,12 @@ int ensure_workspace(srq_exec *e, Workspace &ws, srq_model *m, int32_t n, int32_
     SRQ_CHECK(ensure(ws.LOG, (size_t)sessions * V * 4, e->stream));
     SRQ_CHECK(ensure(ws.ATT, attention_scratch_bytes(n, m->c.heads, m->hd, max_len), e->stream));
     SRQ_CHECK(ensure(ws.PLAN, (size_t)n * 8 + (size_t)n * m->hd * 4, e->stream));
+    // Attention merge counters start at zero; the kernels leave them zero.
+    const size_t cbytes = (size_t)n * m->c.heads * 4;
+    if (cbytes > ws.ATTC.n) {
+        SRQ_CHECK(ensure(ws.ATTC, cbytes, e->stream));
+        SRQ_CHECK(launch_zero(e->stream, as<int32_t>(ws.ATTC), (int64_t)(ws.ATTC.n / 4)));
+    }
     return SRQ_OK;
 }
 

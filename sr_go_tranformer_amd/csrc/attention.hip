@@ -26,6 +26,10 @@ namespace {
 constexpr int kSplit = 64;     // positions per split (two pages)
 constexpr int kMaxGroup = 8;   // query heads per KV head handled together
 constexpr int kMaxHd = 256;
+// Batches up to this many rows use the fused split+merge kernel; larger
+// ones (prefill) the split and combine kernels, whose many workgroups would
+// otherwise each pay the merge's cache write-back and invalidation.
+constexpr int kFusedRows = 4;
 
 __device__ __forceinline__ const float *kv_row(const RowMeta &m, int sess, int pos, int kvdim, int which) {
     const int page = m.pages[(int64_t)sess * m.pt_stride + pos / kPageTokens];
@@ -262,6 +266,174 @@ __global__ __launch_bounds__(256) void attn_split_fast_kernel(const AttnArgs A, 
     }
 }
 
+// Fused split + combine for decode-sized batches, head_dim 64 / 128.
+// Workgroup (row, kv head, split) loads its K and V rows together (one round
+// of memory latency), scores all query heads of the GQA group, writes its
+// partial {m, l, o}, and the last split of a (row, kv head) to finish merges
+// all partials of the group with the combine rule (counter per (row, kv
+// head), reset by the merging workgroup, so the kernel replays without
+// clearing).
+//  scores: thread t -> key t/4 of the split, dims [(t%4)*HD/4, +HD/4)
+//  values: thread t -> dims 4*(t%(HD/4)) .. +3, keys t/(HD/4) + KG*i
+template <int HD>
+__global__ __launch_bounds__(256) void attn_fused_kernel(const AttnArgs A, float *__restrict__ part, int nsplit,
+                                                         int32_t *__restrict__ counters) {
+    constexpr int QD = HD / 4;        // dims per scoring thread
+    constexpr int DG = HD / 4;        // float4 dim groups in the value pass
+    constexpr int KG = 256 / DG;      // key groups in the value pass
+    constexpr int KPG = kSplit / KG;  // keys per value thread
+    __shared__ float qs[kMaxGroup * HD];
+    __shared__ float sc[kMaxGroup][kSplit];
+    __shared__ float4 red[KG][DG];
+    __shared__ float cf[kMaxGroup][64];
+    __shared__ int last;
+
+    const int row = blockIdx.x, kh = blockIdx.y, sp = blockIdx.z;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int kvdim = A.kv_heads * HD, G = A.heads / A.kv_heads;
+    const int pos = A.meta.pos[row], sess = A.meta.sess[row];
+    const int len = pos + 1, s0 = sp * kSplit, s1 = min(len, s0 + kSplit), ns = s1 - s0;
+    if (ns <= 0) return;  // past the row's positions: no partial, no count
+    const int used = (len + kSplit - 1) / kSplit;
+
+    // Page bases of the split's two pages; then every K and V load at once.
+    const int32_t *pt = A.meta.pages + (int64_t)sess * A.meta.pt_stride + s0 / kPageTokens;
+    const float *pb0 = A.meta.kv_pool + (int64_t)pt[0] * A.meta.page_elems +
+                       (int64_t)A.meta.layer * 2 * kPageTokens * kvdim + (int64_t)kh * HD;
+    const float *pb1 = ns > kPageTokens ? A.meta.kv_pool + (int64_t)pt[1] * A.meta.page_elems +
+                                              (int64_t)A.meta.layer * 2 * kPageTokens * kvdim + (int64_t)kh * HD
+                                        : pb0;
+    auto key_row = [&](int s, int which) {  // s < ns
+        const float *pb = s < kPageTokens ? pb0 : pb1;
+        return pb + (int64_t)which * kPageTokens * kvdim + (int64_t)(s & (kPageTokens - 1)) * kvdim;
+    };
+    const int ks = tid >> 2, part4 = tid & 3;
+    float4 kr[QD / 4];
+    {
+        const float *k = key_row(ks < ns ? ks : 0, 0) + part4 * QD;
+#pragma unroll
+        for (int u = 0; u < QD / 4; ++u) kr[u] = ((const float4 *)k)[u];
+    }
+    const int dg = tid % DG, kg = tid / DG;
+    float4 vr[KPG];
+#pragma unroll
+    for (int i = 0; i < KPG; ++i) {
+        const int sv = kg + KG * i;
+        vr[i] = ((const float4 *)key_row(sv < ns ? sv : 0, 1))[dg];
+    }
+    for (int i = tid; i < G * HD; i += 256) {
+        const int g = i / HD, j = i - g * HD;
+        qs[i] = A.q[(int64_t)row * A.heads * HD + (int64_t)(kh * G + g) * HD + j];
+    }
+    __syncthreads();
+    const float scale = (float)(1.0 / sqrt((double)HD));
+
+    // ---- scores -------------------------------------------------------------
+#pragma unroll
+    for (int g = 0; g < kMaxGroup; ++g) {
+        if (g >= G) break;
+        const float *q = qs + g * HD + part4 * QD;
+        float d = 0.0f;
+#pragma unroll
+        for (int u = 0; u < QD / 4; ++u) {
+            d = __builtin_fmaf(q[4 * u + 0], kr[u].x, d);
+            d = __builtin_fmaf(q[4 * u + 1], kr[u].y, d);
+            d = __builtin_fmaf(q[4 * u + 2], kr[u].z, d);
+            d = __builtin_fmaf(q[4 * u + 3], kr[u].w, d);
+        }
+        d += __shfl_xor(d, 1, 64);
+        d += __shfl_xor(d, 2, 64);
+        if (part4 == 0 && ks < ns) sc[g][ks] = d * scale;
+    }
+    __syncthreads();
+
+    // ---- per-head split max and FP64 sum (one wave per head) ----------------
+    for (int g = wave; g < G; g += 4) {
+        float m = -FLT_MAX;
+        if (lane < ns) m = sc[g][lane];
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+        double e = 0.0;
+        if (lane < ns) {
+            e = exp((double)sc[g][lane] - (double)m);
+            sc[g][lane] = (float)e;
+        }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) e += __shfl_xor(e, o, 64);
+        if (lane == 0) {
+            float *p = partial(part, row, kh * G + g, sp, A.heads, nsplit, HD);
+            p[0] = m;
+            *(double *)(p + 2) = e;
+        }
+    }
+    __syncthreads();
+
+    // ---- values ------------------------------------------------------------
+    for (int g = 0; g < G; ++g) {
+        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int i = 0; i < KPG; ++i) {
+            const int sv = kg + KG * i;
+            const float w = sv < ns ? sc[g][sv] : 0.0f;
+            acc.x = __builtin_fmaf(w, vr[i].x, acc.x);
+            acc.y = __builtin_fmaf(w, vr[i].y, acc.y);
+            acc.z = __builtin_fmaf(w, vr[i].z, acc.z);
+            acc.w = __builtin_fmaf(w, vr[i].w, acc.w);
+        }
+        red[kg][dg] = acc;
+        __syncthreads();
+        if (tid < DG) {
+            float4 t = red[0][tid];
+            for (int k2 = 1; k2 < KG; ++k2) {
+                const float4 u = red[k2][tid];
+                t.x += u.x, t.y += u.y, t.z += u.z, t.w += u.w;
+            }
+            float *p = partial(part, row, kh * G + g, sp, A.heads, nsplit, HD);
+            ((float4 *)(p + 4))[tid] = t;
+        }
+        __syncthreads();
+    }
+
+    // ---- the last split of (row, kv head) merges ------------------------------
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");  // publish this split's partials
+    __syncthreads();
+    int32_t *cnt = counters + (int64_t)row * A.kv_heads + kh;
+    if (tid == 0) last = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == used - 1;
+    __syncthreads();
+    if (!last) return;
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    if (tid == 0) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // lse = M + log(sum_i l_i exp(m_i - M)), factors f32(exp(m_i - lse)):
+    // one wave per head, splits in chunks of 64 lanes.
+    for (int g = wave; g < G; g += 4) {
+        const int h = kh * G + g;
+        float M = -FLT_MAX;
+        for (int i = lane; i < used; i += 64) M = fmaxf(M, partial(part, row, h, i, A.heads, nsplit, HD)[0]);
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
+        double l = 0.0;
+        for (int i = lane; i < used; i += 64) {
+            const float *p = partial(part, row, h, i, A.heads, nsplit, HD);
+            l += *(const double *)(p + 2) * exp((double)p[0] - (double)M);
+        }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) l += __shfl_xor(l, o, 64);
+        const double lse = (double)M + log(l);
+        for (int i0 = 0; i0 < used; i0 += 64) {
+            const int i = i0 + lane;
+            if (i < used) cf[g][lane] = (float)exp((double)partial(part, row, h, i, A.heads, nsplit, HD)[0] - lse);
+            // out_j += the chunk's splits, in split order
+            for (int j = lane; j < HD; j += 64) {
+                float o = i0 == 0 ? 0.0f : A.out[(int64_t)row * A.heads * HD + (int64_t)h * HD + j];
+                const int cnt_i = min(64, used - i0);
+                for (int ii = 0; ii < cnt_i; ++ii)
+                    o = __builtin_fmaf(cf[g][ii], partial(part, row, h, i0 + ii, A.heads, nsplit, HD)[4 + j], o);
+                A.out[(int64_t)row * A.heads * HD + (int64_t)h * HD + j] = o;
+            }
+        }
+    }
+}
+
 // lse and the weighted sum of split partials for one (row, head).
 __global__ __launch_bounds__(256) void attn_combine_kernel(const AttnArgs A, const float *__restrict__ part,
                                                            int nsplit) {
@@ -303,7 +475,7 @@ size_t attention_scratch_bytes(int32_t n, int32_t heads, int32_t head_dim, int32
     return (size_t)n * heads * attention_splits(max_len) * (head_dim + 4) * sizeof(float);
 }
 
-int launch_attention(hipStream_t s, const AttnArgs &a, float *scratch) {
+int launch_attention(hipStream_t s, const AttnArgs &a, float *scratch, int32_t *counters) {
     if (a.n <= 0) return SRQ_OK;
     if (a.head_dim > kMaxHd || a.head_dim < 1) return fail(SRQ_EINVAL, "attention: head_dim %d unsupported", a.head_dim);
     const int G = a.heads / a.kv_heads;
@@ -311,6 +483,16 @@ int launch_attention(hipStream_t s, const AttnArgs &a, float *scratch) {
     const int nsplit = attention_splits(a.max_len);
     if (nsplit > 1024) return fail(SRQ_EINVAL, "attention: %d positions exceed the split table", a.max_len);
     const dim3 grid(a.n, a.kv_heads, nsplit);
+    const bool fast = a.head_dim == 128 || a.head_dim == 64;
+    if (fast && a.n <= kFusedRows) {
+        // Decode-sized batches: one launch, the last split merges.
+        if (a.head_dim == 128)
+            attn_fused_kernel<128><<<grid, 256, 0, s>>>(a, scratch, nsplit, counters);
+        else
+            attn_fused_kernel<64><<<grid, 256, 0, s>>>(a, scratch, nsplit, counters);
+        SRQ_HIP(hipGetLastError());
+        return SRQ_OK;
+    }
     if (a.head_dim == 128)
         attn_split_fast_kernel<128><<<grid, 256, 0, s>>>(a, scratch, nsplit);
     else if (a.head_dim == 64)

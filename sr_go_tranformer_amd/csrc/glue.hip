@@ -2,6 +2,8 @@
 // cmd/monolith/monolith.go: rmsInto M:6182-6194, rope M:5264-5289, KV row
 // write M:6393-6395, SwiGLU M:6411-6413, selective-head compaction and
 // expansion M:6420-6448, greedy argmax M:1215-1223.
+#include <algorithm>
+
 #include "srq_internal.h"
 
 namespace srq {
@@ -97,37 +99,79 @@ __global__ __launch_bounds__(256) void gather_kernel(const float *__restrict__ s
 }
 
 // First maximum with strict '>' (lowest id wins ties); non-finite -> err.
-__global__ __launch_bounds__(256) void argmax_kernel(const float *__restrict__ logits, int32_t vocab,
-                                                     int32_t *__restrict__ ids, int32_t *__restrict__ err) {
-    __shared__ float bv[4];
-    __shared__ int bi[4];
+// One 1024-thread workgroup per row; each thread scans its ids in ascending
+// order with 8 float4 loads in flight, then the (value, id) pairs reduce
+// with ties to the lower id.
+constexpr int kArgThreads = 1024;
+
+__device__ __forceinline__ void arg_take(float &best, int &idx, float v, int j) {
+    if (idx < 0 || v > best) best = v, idx = j;
+}
+__device__ __forceinline__ void arg_merge(float &best, int &idx, float ov, int oi) {
+    if (oi >= 0 && (idx < 0 || ov > best || (ov == best && oi < idx))) best = ov, idx = oi;
+}
+
+__global__ __launch_bounds__(kArgThreads) void argmax_kernel(const float *__restrict__ logits, int32_t vocab,
+                                                             int32_t *__restrict__ ids, int32_t *__restrict__ err) {
+    constexpr int NW = kArgThreads / 64, U = 8;
+    __shared__ float bv[NW];
+    __shared__ int bi[NW];
     __shared__ int bad;
-    if (threadIdx.x == 0) bad = 0;
+    const int tid = threadIdx.x;
+    if (tid == 0) bad = 0;
     __syncthreads();
     const float *row = logits + (int64_t)blockIdx.x * vocab;
     float best = 0.0f;
     int idx = -1;
     int nonfinite = 0;
-    for (int j = threadIdx.x; j < vocab; j += 256) {
-        const float v = row[j];
-        if (!isfinite(v)) nonfinite = 1;
-        if (idx < 0 || v > best) best = v, idx = j;  // ascending j per thread
+    if ((vocab & 3) == 0) {
+        const int n4 = vocab / 4;
+        for (int base = 0; base < n4; base += kArgThreads * U) {
+            float4 t[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int j4 = base + u * kArgThreads + tid;
+                t[u] = j4 < n4 ? ((const float4 *)row)[j4] : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int j4 = base + u * kArgThreads + tid;
+                if (j4 >= n4) continue;
+                const float v[4] = {t[u].x, t[u].y, t[u].z, t[u].w};
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    nonfinite |= !isfinite(v[c]);
+                    arg_take(best, idx, v[c], 4 * j4 + c);
+                }
+            }
+        }
+    } else {
+        for (int base = 0; base < vocab; base += kArgThreads * U) {
+            float t[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int j = base + u * kArgThreads + tid;
+                t[u] = j < vocab ? row[j] : 0.0f;
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int j = base + u * kArgThreads + tid;
+                if (j >= vocab) continue;
+                nonfinite |= !isfinite(t[u]);
+                arg_take(best, idx, t[u], j);
+            }
+        }
     }
     if (nonfinite) bad = 1;
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        const float ov = __shfl_xor(best, o, 64);
-        const int oi = __shfl_xor(idx, o, 64);
-        if (oi >= 0 && (idx < 0 || ov > best || (ov == best && oi < idx))) best = ov, idx = oi;
-    }
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    for (int o = 32; o > 0; o >>= 1) arg_merge(best, idx, __shfl_xor(best, o, 64), __shfl_xor(idx, o, 64));
+    const int lane = tid & 63, wave = tid >> 6;
     if (lane == 0) bv[wave] = best, bi[wave] = idx;
     __syncthreads();
-    if (threadIdx.x == 0) {
+    if (tid == 0) {
         float b = bv[0];
         int i = bi[0];
-        for (int w = 1; w < 4; ++w)
-            if (bi[w] >= 0 && (i < 0 || bv[w] > b || (bv[w] == b && bi[w] < i))) b = bv[w], i = bi[w];
+        for (int w = 1; w < NW; ++w) arg_merge(b, i, bv[w], bi[w]);
         ids[blockIdx.x] = i;
         if (bad) err[0] = 1;
     }
@@ -162,7 +206,20 @@ __global__ void row_plan_kernel(const int32_t *pos, const int32_t *sess, const i
     }
 }
 
+__global__ void zero_kernel(int32_t *dst, int64_t count) {
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < count; i += (int64_t)gridDim.x * blockDim.x)
+        dst[i] = 0;
+}
+
 }  // namespace
+
+int launch_zero(hipStream_t s, int32_t *dst, int64_t count) {
+    if (count <= 0) return SRQ_OK;
+    const int64_t blocks = std::min<int64_t>((count + 255) / 256, 1024);
+    zero_kernel<<<(unsigned)blocks, 256, 0, s>>>(dst, count);
+    SRQ_HIP(hipGetLastError());
+    return SRQ_OK;
+}
 
 int launch_row_plan(hipStream_t s, const RowMeta &meta, int32_t n, int32_t kvdim, int32_t head_dim,
                     const float *cos_t, const float *sin_t, int64_t *kvoff, float *rope_cs) {
@@ -208,7 +265,7 @@ int launch_gather_rows(hipStream_t s, const float *src, int64_t d, const int32_t
 
 int launch_argmax(hipStream_t s, const float *logits, int32_t rows, int32_t vocab, int32_t *ids, int32_t *err) {
     if (rows <= 0) return SRQ_OK;
-    argmax_kernel<<<rows, 256, 0, s>>>(logits, vocab, ids, err);
+    argmax_kernel<<<rows, kArgThreads, 0, s>>>(logits, vocab, ids, err);
     SRQ_HIP(hipGetLastError());
     return SRQ_OK;
 }

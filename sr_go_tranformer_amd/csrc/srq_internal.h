@@ -57,6 +57,7 @@ int launch_convert_f32(hipStream_t s, int64_t count, const void *src, int dtype,
 int launch_dequant_rows(hipStream_t s, int fmt, int64_t cols, const void *values, const float *scales,
                         const int32_t *rows, int32_t count, float *dst);
 int launch_fill_normal(hipStream_t s, float *dst, int64_t count, uint64_t seed, double scale);
+int launch_zero(hipStream_t s, int32_t *dst, int64_t count);
 
 // ------------------------------------------------------------------ GEMV
 enum Epilogue { EPI_PLAIN = 0, EPI_RESID = 1, EPI_SWIGLU = 2, EPI_ROPE_KV = 3 };
@@ -145,8 +146,10 @@ struct AttnArgs {
     int32_t max_len;    // upper bound of pos+1 over rows (sizes LDS)
     RowMeta meta;
 };
-// scratch: attention_scratch_bytes(n, heads, head_dim, max_len) bytes.
-int launch_attention(hipStream_t s, const AttnArgs &a, float *scratch);
+// scratch: attention_scratch_bytes(n, heads, head_dim, max_len) bytes;
+// counters: n*heads int32, zero before the first launch (the kernels leave
+// them zero).
+int launch_attention(hipStream_t s, const AttnArgs &a, float *scratch, int32_t *counters);
 size_t attention_scratch_bytes(int32_t n, int32_t heads, int32_t head_dim, int32_t max_len);
 int attention_prepare();
 

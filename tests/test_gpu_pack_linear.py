@@ -238,3 +238,37 @@ def test_linear_rejects_bad_arguments(ex):
     import ctypes as C
     assert srq.lib().srq_linear(ex.h, b.ptr, b.ptr, w.h, 1) == srq.EINVAL
     assert srq.lib().srq_linear(ex.h, b.ptr, C.c_void_p(b.value + 64), w.h, 1025) == srq.EINVAL
+
+
+def _device_argmax(ex, logits):
+    import ctypes as C
+    rows, vocab = logits.shape
+    buf = srq.DeviceBuffer.from_numpy(ex, np.ascontiguousarray(logits, np.float32))
+    ids = np.zeros(rows, np.int32)
+    srq.check(srq.lib().srq_argmax(ex.h, buf.ptr, rows, vocab, ids.ctypes.data_as(C.c_void_p)))
+    return ids
+
+
+@pytest.mark.parametrize("vocab", [1, 3, 4, 5, 1000, 4097, 32768, 50257, 128256])
+def test_argmax_lowest_id_wins_ties(ex, vocab):
+    """sampleWithBlocked at T=0 (M:7331-7358): strict '>' scan, so the first
+    (lowest) id of the maximum wins; np.argmax has the same rule."""
+    rng = np.random.default_rng(vocab)
+    rows = 3
+    logits = rng.integers(-50, 50, size=(rows, vocab)).astype(np.float32)  # many exact ties
+    logits[1, :] = 7.0  # all equal: id 0
+    if vocab > 10:
+        logits[2, vocab - 1] = 1000.0
+        logits[2, vocab // 2] = 1000.0  # tie between two far-apart ids
+    assert np.array_equal(_device_argmax(ex, logits), np.argmax(logits, axis=1))
+
+
+def test_argmax_rejects_nonfinite(ex):
+    logits = np.zeros((2, 777), np.float32)
+    for bad in (np.inf, -np.inf, np.nan):
+        logits[1, 500] = bad
+        with pytest.raises(srq.SrqError) as e:
+            _device_argmax(ex, logits)
+        assert e.value.code == srq.ENONFINITE
+        logits[1, 500] = 0.0
+    assert list(_device_argmax(ex, logits)) == [0, 0]
