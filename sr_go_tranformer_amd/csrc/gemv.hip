@@ -576,7 +576,9 @@ __device__ __forceinline__ void stage_stream(const GemvArgs &A, float *lds, cons
     for (int b = 0; b < NB; ++b) ss[b] = 0.0;
     const bool vec = ((((uintptr_t)A.x) | (NORM ? (uintptr_t)A.norm_w : 0)) & 15) == 0 && (cols & 3) == 0;
     if (vec) {
-        constexpr int U = NB >= 4 ? 1 : 4 / NB;  // float4 loads in flight per row: 4 rows' worth
+        // float4 loads in flight per thread: 8 rows' worth, so one pass
+        // stages a 16384-column single row (the 14336-wide down input).
+        constexpr int U = NB >= 8 ? 1 : 8 / NB;
         for (int c0 = tid * 4; c0 < ld; c0 += NT * 4 * U) {
             float4 t[NB][U], w[U];
 #pragma unroll
