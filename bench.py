@@ -188,6 +188,158 @@ def cpu_baseline(srq, ex, model, cfg, cache, first, gpu_tokens, n_tokens):
     return runs, setup_s
 
 
+def percentiles(us):
+    a = np.sort(np.asarray(us, np.float64))
+    return float(np.median(a)), float(a[int(0.1 * (len(a) - 1))]), float(a[int(0.9 * (len(a) - 1))])
+
+
+def bench_smollm2(srq, args):
+    """SmolLM2-135M architecture (576 / 30 layers / 9:3 heads / 1536 /
+    49152 tied), Q8, seeded N(0, 0.02) weights: 32-token random prompt, then
+    64 greedy tokens (graph-replayed decode).  Tokens/s over the 63 replayed
+    decode steps of a second generation (the first warms the graph)."""
+    from sr_go_tranformer_amd import synthetic
+    ex = srq.Executor(0)
+    cfg = synthetic.shape_config("smollm2-135m", 2048)
+    model = synthetic.build(ex, cfg, "q8", args.seed)
+    hip = HipEvents()
+    stream = C.c_void_p(ex.stream)
+    pool = model.pool(8)
+    prompt = synthetic.random_prompt(32, cfg.vocab, args.seed)
+    times, tokens = [], None
+    for rep in range(3):
+        cache = pool.cache(4)
+        model.step([cache], [prompt])
+        first = int(model.argmax_last()[0])
+        dec = srq.Decoder(model, cache, first, 63)
+        ex.synchronize()
+        a, b = hip.create(), hip.create()
+        hip.record(a, stream)
+        dec.run(63)
+        hip.record(b, stream)
+        times.append(hip.elapsed_ms(a, b))
+        tokens = [first] + dec.tokens()
+        dec.close()
+        cache.close()
+    ms = min(times[1:])
+    wbytes = synthetic.decode_weight_bytes(cfg, "q8")
+    tps = 63 / (ms / 1e3)
+    print(json.dumps({
+        "metric": "SmolLM2-135M-shape Q8 greedy decode tokens/s, batch 1", "value": round(tps, 1),
+        "unit": "tokens/s", "n_gpus": 1, "higher_is_better": True, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": "SmolLM2-135M-shape Q8, 32-token random prompt, 64 greedy tokens (63 timed "
+                               "graph-replayed decode steps)", "seed": args.seed},
+        "ms_per_token": round(ms / 63, 4), "weight_bytes_per_token": wbytes,
+        "weight_gbs": round(wbytes * tps / 1e9, 1), "tokens": tokens}), flush=True)
+    return 0
+
+
+def bench_gemv_sweep(srq, args):
+    """Isolated Q8 dequant-GEMV at Llama-3.2-1B shapes (hidden 2048,
+    intermediate 8192, vocab 128256): weights N(0, 0.02) packed on the
+    device, x N(0, 1), batch 1 / 4 / 16, 200 timed launches each (HIP
+    events around every launch, on the launch stream): median, p10, p90."""
+    ex = srq.Executor(0)
+    hip = HipEvents()
+    stream = C.c_void_p(ex.stream)
+    L = srq.lib()
+    shapes = [("q_proj/o_proj", 2048, 2048), ("k_proj/v_proj", 512, 2048), ("gate_proj/up_proj", 8192, 2048),
+              ("down_proj", 2048, 8192), ("lm_head", 128256, 2048)]
+    out = []
+    for t, (name, rows, cols) in enumerate(shapes):
+        src = ex.empty(rows * cols * 4)
+        srq.fill_normal(ex, src, rows * cols, args.seed * 1000003 + t, 0.02)
+        h = C.c_void_p()
+        srq.check(L.srq_weight_create(ex.h, srq.Q8, rows, cols, src.ptr, srq.SRC_F32, C.byref(h)))
+        w = srq.Weight(h)
+        src.close()
+        vb, sb = srq.packed_bytes(srq.Q8, rows, cols)
+        for n in (1, 4, 16):
+            x = ex.empty(n * cols * 4)
+            srq.fill_normal(ex, x, n * cols, 7 + n, 1.0)
+            y = ex.empty(n * rows * 4)
+            for _ in range(10):
+                srq.check(L.srq_linear_enqueue(ex.h, y.ptr, x.ptr, w.h, n))
+            ex.synchronize()
+            evs = [(hip.create(), hip.create()) for _ in range(200)]
+            for a, b in evs:
+                hip.record(a, stream)
+                srq.check(L.srq_linear_enqueue(ex.h, y.ptr, x.ptr, w.h, n))
+                hip.record(b, stream)
+            ex.synchronize()
+            us = [hip.elapsed_ms(a, b) * 1e3 for a, b in evs]
+            for a, b in evs:
+                hip.destroy(a)
+                hip.destroy(b)
+            med, p10, p90 = percentiles(us)
+            algo = vb + sb + n * cols * 4 + n * rows * 4
+            out.append({"matrix": name, "rows": rows, "cols": cols, "n": n, "median_us": round(med, 3),
+                        "p10_us": round(p10, 3), "p90_us": round(p90, 3), "algorithmic_bytes": algo,
+                        "gbs_median": round(algo / (med * 1e-6) / 1e9, 1),
+                        "frac_of_hbm_peak": round(algo / (med * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                        "gflops_median": round(2.0 * n * rows * cols / (med * 1e-6) / 1e9, 1)})
+            x.close()
+            y.close()
+        w.close()
+    print(json.dumps({"metric": "Q8 dequant-GEMV sweep at Llama-3.2-1B shapes (per launch, HIP events)",
+                      "unit": "us", "n_gpus": 1, "higher_is_better": False, "dtype": "f32", "data": "synthetic",
+                      "config": {"workload": "Llama-3.2-1B matrices, Q8, batch 1/4/16, 200 launches each",
+                                 "seed": args.seed}, "results": out}), flush=True)
+    return 0
+
+
+def bench_q4mixed_prefill(srq, args):
+    """Mistral-7B shape, q4-mixed (Q4 layer matrices, Q8 embedding and
+    head): a 2048-token random prompt prefilled in 256-token chunks (MFMA
+    dequant-GEMM, head only on each chunk's last row), then 128 greedy
+    decode tokens."""
+    from sr_go_tranformer_amd import synthetic
+    ex = srq.Executor(0)
+    prompt_n, chunk, gen = 2048, 256, 128
+    cfg = synthetic.shape_config("mistral-7b", prompt_n + gen)
+    model = synthetic.build(ex, cfg, "q4-mixed", args.seed)
+    hip = HipEvents()
+    stream = C.c_void_p(ex.stream)
+    pool = model.pool((prompt_n + gen) // 32 + 2)
+    cache = pool.cache((prompt_n + gen + 31) // 32)
+    prompt = synthetic.random_prompt(prompt_n, cfg.vocab, args.seed)
+    ex.synchronize()
+    chunk_ms = []
+    for lo in range(0, prompt_n, chunk):
+        a, b = hip.create(), hip.create()
+        hip.record(a, stream)
+        model.step([cache], [prompt[lo:lo + chunk]])
+        hip.record(b, stream)
+        chunk_ms.append(hip.elapsed_ms(a, b))
+    first = int(model.argmax_last()[0])
+    dec = srq.Decoder(model, cache, first, gen - 1)
+    ex.synchronize()
+    a, b = hip.create(), hip.create()
+    hip.record(a, stream)
+    dec.run(gen - 1)
+    hip.record(b, stream)
+    dec_ms = hip.elapsed_ms(a, b)
+    dec.close()
+    d, kd, H, V = cfg.dim, cfg.dim // cfg.heads * cfg.kv_heads, cfg.hidden, cfg.vocab
+    params = cfg.layers * ((d + 2 * kd) * d + d * d + 2 * H * d + d * H)
+    flops_chunk = 2.0 * chunk * params + 2.0 * d * V  # layer GEMMs + one head row
+    prefill_s = sum(chunk_ms) / 1e3
+    print(json.dumps({
+        "metric": "Mistral-7B-shape Q4-mixed chunked prefill tokens/s (256-token chunks) + decode tokens/s",
+        "value": round(prompt_n / prefill_s, 1), "unit": "tokens/s", "n_gpus": 1, "higher_is_better": True,
+        "dtype": "f32", "data": "synthetic",
+        "config": {"workload": "Mistral-7B shape, q4-mixed, 2048 random prompt tokens in 256-token chunks, "
+                               "then 128 greedy tokens", "seed": args.seed},
+        "chunk_ms": [round(t, 2) for t in chunk_ms],
+        "layer_gemm_tflops_per_chunk": round(2.0 * chunk * params / 1e12, 3),
+        "achieved_tflops_mean": round(flops_chunk * len(chunk_ms) / prefill_s / 1e12, 2),
+        "fp32_mfma_peak_tflops": 157.3,
+        "decode_tokens_per_s": round((gen - 1) / (dec_ms / 1e3), 1),
+        "decode_weight_bytes_per_token": synthetic.decode_weight_bytes(cfg, "q4-mixed"),
+        "resident_weight_bytes": model.resident_bytes()}), flush=True)
+    return 0
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -197,6 +349,10 @@ def main():
     ap.add_argument("--cpu-tokens", type=int, default=6, help="decode tokens of the CPU baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--gemv-launches", type=int, default=320)
+    ap.add_argument("--config", default="mistral7b-q8-decode",
+                    choices=["mistral7b-q8-decode", "smollm2-q8-decode", "llama1b-q8-gemv-sweep",
+                             "mistral7b-q4mixed-prefill"],
+                    help="workload; the default is the headline Mistral-7B Q8 decode")
     ap.add_argument("--gemv-only", action="store_true",
                     help="run only the GEMV roofline leg (standalone weights) and a calibration copy")
     ap.add_argument("--eager", action="store_true",
@@ -216,6 +372,12 @@ def main():
 
     if args.gemv_only:
         return gemv_only(srq, args.gemv_launches, args.seed)
+    if args.config == "smollm2-q8-decode":
+        return bench_smollm2(srq, args)
+    if args.config == "llama1b-q8-gemv-sweep":
+        return bench_gemv_sweep(srq, args)
+    if args.config == "mistral7b-q4mixed-prefill":
+        return bench_q4mixed_prefill(srq, args)
 
     t_start = time.perf_counter()
     ex = srq.Executor(0)

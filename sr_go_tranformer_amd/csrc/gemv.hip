@@ -969,11 +969,11 @@ int launch_t(hipStream_t s, const GemvArgs &a) {
     }
 }
 
-// Widest streaming launch: 4 batch rows (Q4: 2, whose 32 codes per lane
+// Widest streaming launch: 8 batch rows (Q4: 2, whose 32 codes per lane
 // per chunk leave fewer registers); the generic kernel takes 8.
 template <int FMT, bool FAST>
 constexpr int max_nb() {
-    return !FAST ? 8 : FMT == SRQ_Q4 ? 2 : 4;
+    return !FAST ? 8 : FMT == SRQ_Q4 ? 2 : 8;
 }
 
 template <int FMT, bool FAST, int EPI, bool NORM>
@@ -1063,10 +1063,10 @@ int gemv_max_rows(int fmt, int64_t cols, bool norm, int64_t extra_floats) {
     const bool fast = gemv_fast_ok(fmt, cols);
     const int64_t cw = !fast ? 256 : fmt == SRQ_Q8 ? 1024 : fmt == SRQ_Q4 ? 2048 : 256;
     const int64_t ld = (cols + cw - 1) / cw * cw;
-    // Fast layouts stream at most 4 rows per launch (Q4: 2); larger batches
+    // Fast layouts stream at most 8 rows per launch (Q4: 2); larger batches
     // are chunked by the caller.  Their LDS also holds the norm weight and
     // the epilogue's per-row data (extra_floats bounds it).
-    for (int nb = !fast ? 8 : fmt == SRQ_Q4 ? 2 : 4; nb >= 1; nb /= 2) {
+    for (int nb = !fast ? 8 : fmt == SRQ_Q4 ? 2 : 8; nb >= 1; nb /= 2) {
         const int64_t floats = fast ? nb * ld + (norm ? ld : 0) + extra_floats : nb * ld;
         if (floats * 4 <= (int64_t)kMaxLds) return nb;
     }
