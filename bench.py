@@ -295,7 +295,7 @@ def bench_q4mixed_prefill(srq, args):
     decode tokens."""
     from sr_go_tranformer_amd import synthetic
     ex = srq.Executor(0)
-    prompt_n, chunk, gen = 2048, 256, 128
+    prompt_n, chunk, gen = args.prompt_tokens, 256, args.gen_tokens
     cfg = synthetic.shape_config("mistral-7b", prompt_n + gen)
     model = synthetic.build(ex, cfg, "q4-mixed", args.seed)
     hip = HipEvents()
@@ -328,8 +328,8 @@ def bench_q4mixed_prefill(srq, args):
         "metric": "Mistral-7B-shape Q4-mixed chunked prefill tokens/s (256-token chunks) + decode tokens/s",
         "value": round(prompt_n / prefill_s, 1), "unit": "tokens/s", "n_gpus": 1, "higher_is_better": True,
         "dtype": "f32", "data": "synthetic",
-        "config": {"workload": "Mistral-7B shape, q4-mixed, 2048 random prompt tokens in 256-token chunks, "
-                               "then 128 greedy tokens", "seed": args.seed},
+        "config": {"workload": "Mistral-7B shape, q4-mixed, %d random prompt tokens in 256-token chunks, "
+                               "then %d greedy tokens" % (prompt_n, gen), "seed": args.seed},
         "chunk_ms": [round(t, 2) for t in chunk_ms],
         "layer_gemm_tflops_per_chunk": round(2.0 * chunk * params / 1e12, 3),
         "achieved_tflops_mean": round(flops_chunk * len(chunk_ms) / prefill_s / 1e12, 2),
@@ -353,6 +353,8 @@ def main():
                     choices=["mistral7b-q8-decode", "smollm2-q8-decode", "llama1b-q8-gemv-sweep",
                              "mistral7b-q4mixed-prefill"],
                     help="workload; the default is the headline Mistral-7B Q8 decode")
+    ap.add_argument("--prompt-tokens", type=int, default=2048, help="mistral7b-q4mixed-prefill: prompt length")
+    ap.add_argument("--gen-tokens", type=int, default=128, help="mistral7b-q4mixed-prefill: generated tokens")
     ap.add_argument("--gemv-only", action="store_true",
                     help="run only the GEMV roofline leg (standalone weights) and a calibration copy")
     ap.add_argument("--eager", action="store_true",
