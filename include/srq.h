@@ -147,7 +147,11 @@ enum {
     SRQ_T_DOWN = 18,      /* mlp.down_proj               [dim x hidden]  */
     SRQ_T_Q_BIAS = 19,    /* self_attn.q_proj.bias       [dim]           */
     SRQ_T_K_BIAS = 20,    /* self_attn.k_proj.bias       [kvdim]         */
-    SRQ_T_V_BIAS = 21     /* self_attn.v_proj.bias       [kvdim]         */
+    SRQ_T_V_BIAS = 21,    /* self_attn.v_proj.bias       [kvdim]         */
+    /* srq_model_weight only (no counterpart in the reference's specs): the
+     * fused matrices a step streams. */
+    SRQ_T_QKV = 22,       /* q, k, v rows stacked       [dim+2*kvdim x dim] */
+    SRQ_T_GATE_UP = 23    /* gate rows, then up rows    [2*hidden x dim] */
 };
 
 /* weight_format: "f32", "q8", "q4" or "q4-mixed" (M:566-582: q4-mixed keeps
@@ -158,7 +162,8 @@ int srq_model_load(srq_model *m, int kind, int layer, const void *src, srq_src_d
 int srq_model_destroy(srq_model *m);
 /* hfWeightLayoutFor byte accounting (M:591-619) of the resident weights. */
 int srq_model_resident_bytes(const srq_model *m, int64_t *bytes);
-/* Borrow a view of one matrix (valid while the model lives). */
+/* Borrow a view of one matrix (valid while the model lives); SRQ_T_QKV and
+ * SRQ_T_GATE_UP give the fused storage. */
 int srq_model_weight(srq_model *m, int kind, int layer, srq_weight **out);
 /* The FP32 RoPE tables (M:5034-5043), [context x head_dim/2] each, host. */
 int srq_model_rope_tables(const srq_model *m, float *cos_out, float *sin_out);

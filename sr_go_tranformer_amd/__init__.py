@@ -23,6 +23,7 @@ SRC_F32, SRC_BF16, SRC_F16 = 0, 1, 2
 OK, EDEVICE, ENOMEM, EINVAL, ENOSPC, ENONFINITE, ERANGE, ECANCELED = 0, -5, -12, -22, -28, -33, -34, -125
 T_EMBED, T_FINAL_NORM, T_OUTPUT = 0, 1, 2
 T_ATTN_NORM, T_Q, T_K, T_V, T_O, T_FFN_NORM, T_GATE, T_UP, T_DOWN, T_Q_BIAS, T_K_BIAS, T_V_BIAS = range(10, 22)
+T_QKV, T_GATE_UP = 22, 23  # fused storage views (srq_model_weight only)
 
 FORMATS = {"f32": F32, "q8": Q8, "q4": Q4}
 

@@ -661,7 +661,13 @@ static srq_weight *model_matrix(srq_model *m, int kind, int layer) {
 
 int srq_model_weight(srq_model *m, int kind, int layer, srq_weight **out) {
     if (!m || !out) return fail(SRQ_EINVAL, "null pointer");
-    srq_weight *w = model_matrix(m, kind, layer);
+    srq_weight *w = nullptr;
+    if (kind == SRQ_T_QKV || kind == SRQ_T_GATE_UP) {
+        // The fused storage the step streams (borrow only).
+        if (layer >= 0 && layer < m->c.layers) w = kind == SRQ_T_QKV ? &m->L[layer].qkv : &m->L[layer].gu;
+    } else {
+        w = model_matrix(m, kind, layer);
+    }
     if (!w) return fail(SRQ_EINVAL, "no matrix of kind %d at layer %d", kind, layer);
     *out = w;
     return SRQ_OK;

@@ -191,3 +191,25 @@ def test_fill_normal_matches_serial_rng(ex):
     want = oracle.RNG(12345).fill_normal(100000, 0.02)
     diff = got.view(np.int32).astype(np.int64) - want.view(np.int32).astype(np.int64)
     assert np.abs(diff).max() <= 1 and (diff != 0).mean() < 1e-3
+
+
+def test_fused_storage_views(ex):
+    """SRQ_T_QKV / SRQ_T_GATE_UP borrow the fused matrices the step streams:
+    their rows are the q, k, v (gate, up) rows, so a GEMV over the fused view
+    equals the per-matrix GEMVs bit for bit."""
+    fx = hf_fixtures.load("mistral_f32")
+    m = gpu_models.load_fixture(ex, fx, "q8")
+    x = np.random.default_rng(3).normal(size=(2, fx.dim)).astype(np.float32)
+    for layer in (0, fx.layers - 1):
+        gu = m.weight(srq.T_GATE_UP, layer)
+        assert (gu.rows, gu.cols) == (2 * fx.hidden, fx.dim)
+        got = srq.linear(ex, gu, x)
+        want = np.concatenate([srq.linear(ex, m.weight(srq.T_GATE, layer), x),
+                               srq.linear(ex, m.weight(srq.T_UP, layer), x)], axis=1)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+        qkv = m.weight(srq.T_QKV, layer)
+        got = srq.linear(ex, qkv, x)
+        want = np.concatenate([srq.linear(ex, m.weight(k, layer), x) for k in (srq.T_Q, srq.T_K, srq.T_V)], axis=1)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    with pytest.raises(srq.SrqError):
+        m.weight(srq.T_GATE_UP, fx.layers)
