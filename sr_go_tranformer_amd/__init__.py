@@ -63,7 +63,7 @@ EXPORTS = [
     "srq_weight_destroy", "srq_weight_info", "srq_dequant_rows", "srq_linear", "srq_linear_enqueue", "srq_model_create",
     "srq_model_load", "srq_model_destroy", "srq_model_resident_bytes", "srq_model_weight",
     "srq_model_rope_tables", "srq_pool_create", "srq_pool_destroy", "srq_cache_create", "srq_cache_destroy",
-    "srq_cache_pos", "srq_cache_read", "srq_step", "srq_argmax", "srq_decoder_create", "srq_decoder_run",
+    "srq_cache_pos", "srq_cache_read", "srq_step", "srq_argmax", "srq_sample", "srq_decoder_create", "srq_decoder_run",
     "srq_decoder_tokens", "srq_decoder_destroy", "srq_generate_greedy",
 ]
 
@@ -108,6 +108,7 @@ def _declare(L):
         "srq_cache_read": (C.c_int, [P, P, I32, I32, I32, P, P]),
         "srq_step": (C.c_int, [P, P, I32, P, P, P, P, PP, P, P]),
         "srq_argmax": (C.c_int, [P, P, I32, I32, P]),
+        "srq_sample": (C.c_int, [P, P, I32, I32, P, P, P, I32, P, P, P]),
         "srq_decoder_create": (C.c_int, [P, P, P, I32, I32, I32, PP]),
         "srq_decoder_run": (C.c_int, [P, I32]),
         "srq_decoder_tokens": (C.c_int, [P, P, C.POINTER(I32)]),
@@ -442,6 +443,35 @@ class Cache:
             self.close()
         except Exception:
             pass
+
+
+class Sampling(C.Structure):
+    """srq_sampling: temperature (0: greedy), top_k (0: off), top_p (>= 1:
+    off), repeat_penalty (1: off)."""
+    _fields_ = [("temperature", C.c_double), ("top_k", C.c_int32), ("top_p", C.c_double),
+                ("repeat_penalty", C.c_double)]
+
+
+def sample(ex, logits_ptr, rows, vocab, params, rng_states, histories=None, blocked=None):
+    """srq_sample over device logits; rng_states (np.uint64 [rows]) is
+    advanced in place; histories: list of per-row id lists or None."""
+    rng = np.ascontiguousarray(rng_states, np.uint64)
+    assert rng.shape == (rows,) and rng is rng_states, "rng_states must be a contiguous uint64 array"
+    ids = np.zeros(rows, np.int32)
+    hist = hl = None
+    stride = 0
+    if histories is not None:
+        stride = max(1, max(len(h) for h in histories))
+        hist = np.zeros((rows, stride), np.int32)
+        hl = np.zeros(rows, np.int32)
+        for r, h in enumerate(histories):
+            hist[r, :len(h)] = h
+            hl[r] = len(h)
+    blk = None if blocked is None else np.ascontiguousarray(blocked, np.int32)
+    ptr = lambda a: None if a is None else _np_ptr(a)
+    check(lib().srq_sample(ex.h, logits_ptr, rows, vocab, C.byref(params), ptr(hist), ptr(hl), stride, ptr(blk),
+                           _np_ptr(rng), _np_ptr(ids)))
+    return ids
 
 
 class Decoder:

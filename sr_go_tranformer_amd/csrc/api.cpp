@@ -121,9 +121,10 @@ using namespace srq;
 // M:6062-6100).  Captured graphs point into a decoder's own workspace, so a
 // later step that grows the executor's workspace cannot invalidate them.
 struct Workspace {
-    DevBuf X, N, Q, A, T, H, W2, LOG, LOGC, meta, flags, ATT, ATTC, PLAN;
+    DevBuf X, N, Q, A, T, H, W2, LOG, LOGC, meta, flags, ATT, ATTC, PLAN, SMP, SMPP;
     void release_all() {
-        for (DevBuf *b : {&X, &N, &Q, &A, &T, &H, &W2, &LOG, &LOGC, &meta, &flags, &ATT, &ATTC, &PLAN}) release(*b);
+        for (DevBuf *b : {&X, &N, &Q, &A, &T, &H, &W2, &LOG, &LOGC, &meta, &flags, &ATT, &ATTC, &PLAN, &SMP, &SMPP})
+            release(*b);
     }
 };
 
@@ -1121,7 +1122,65 @@ extern "C" int srq_argmax(srq_exec *e, const float *logits, int32_t rows, int32_
     return check_err_flag(e, SRQ_ENONFINITE, "non-finite HF logits");
 }
 
-// ----------------------------------------------------------- greedy decoder
+extern "C" int srq_sample(srq_exec *e, const float *logits, int32_t rows, int32_t vocab, const srq_sampling *params,
+                          const int32_t *history, const int32_t *history_len, int32_t history_stride,
+                          const int32_t *blocked, uint64_t *rng_state, int32_t *ids) {
+    if (!e || !logits || !params || !rng_state || !ids) return fail(SRQ_EINVAL, "null pointer");
+    if (rows < 1 || vocab < 1) return fail(SRQ_EINVAL, "empty logits");
+    if (!(params->temperature >= 0) || !(params->repeat_penalty > 0) || params->top_k < 0 || !(params->top_p > 0))
+        return fail(SRQ_EINVAL, "bad sampling parameters");
+    if (history && (!history_len || history_stride < 0)) return fail(SRQ_EINVAL, "history without lengths");
+    for (int32_t r = 0; history && r < rows; ++r)
+        if (history_len[r] < 0 || history_len[r] > history_stride) return fail(SRQ_EINVAL, "bad history length");
+    DeviceGuard g(e->device);
+    Workspace &ws = e->ws;
+    const size_t hist_words = history ? (size_t)rows * history_stride : 0;
+    // [rng: 2*rows][ids: rows][blocked: rows][history_len: rows][history]
+    const size_t words = (size_t)rows * 5 + hist_words;
+    SRQ_CHECK(ensure(ws.SMP, words * 4, e->stream));
+    SRQ_CHECK(ensure(ws.SMPP, sample_scratch_bytes(rows, vocab), e->stream));
+    int32_t *d = as<int32_t>(ws.SMP);
+    uint64_t *d_rng = (uint64_t *)d;
+    int32_t *d_ids = d + 2 * rows, *d_blk = d + 3 * rows, *d_hl = d + 4 * rows, *d_hist = d + 5 * rows;
+    SRQ_HIP(hipMemcpyAsync(d_rng, rng_state, (size_t)rows * 8, hipMemcpyHostToDevice, e->stream));
+    if (blocked) SRQ_HIP(hipMemcpyAsync(d_blk, blocked, (size_t)rows * 4, hipMemcpyHostToDevice, e->stream));
+    if (history) {
+        SRQ_HIP(hipMemcpyAsync(d_hl, history_len, (size_t)rows * 4, hipMemcpyHostToDevice, e->stream));
+        if (hist_words)
+            SRQ_HIP(hipMemcpyAsync(d_hist, history, hist_words * 4, hipMemcpyHostToDevice, e->stream));
+    }
+    SampleArgs a{};
+    a.logits = logits;
+    a.rows = rows;
+    a.vocab = vocab;
+    a.temperature = params->temperature;
+    a.top_k = params->top_k;
+    a.top_p = params->top_p;
+    a.repeat_penalty = params->repeat_penalty;
+    a.history = history ? d_hist : nullptr;
+    a.history_len = history ? d_hl : nullptr;
+    a.history_stride = history_stride;
+    a.blocked = blocked ? d_blk : nullptr;
+    a.rng = d_rng;
+    a.ids = d_ids;
+    a.err = e->d_err;
+    SRQ_CHECK(launch_sample(e->stream, a, ws.SMPP.p));
+    SRQ_HIP(hipMemcpyAsync(ids, d_ids, (size_t)rows * 4, hipMemcpyDeviceToHost, e->stream));
+    SRQ_HIP(hipMemcpyAsync(rng_state, d_rng, (size_t)rows * 8, hipMemcpyDeviceToHost, e->stream));
+    SRQ_HIP(hipMemcpyAsync(e->h_err, e->d_err, sizeof(int32_t) * 4, hipMemcpyDeviceToHost, e->stream));
+    SRQ_HIP(hipStreamSynchronize(e->stream));
+    const int32_t err = e->h_err[0];
+    if (err) {
+        SRQ_HIP(hipMemsetAsync(e->d_err, 0, sizeof(int32_t) * 4, e->stream));
+        SRQ_HIP(hipStreamSynchronize(e->stream));
+        if (err & 1) return fail(SRQ_ENONFINITE, "non-finite logits");
+        if (err & 2) return fail(SRQ_EINVAL, "no candidate token");
+        return fail(SRQ_EINVAL, "sampling selection limit exceeded (more than 2048 equal-ranked candidates)");
+    }
+    return SRQ_OK;
+}
+
+// ----------------------------------------------------------- greedy decoder// ----------------------------------------------------------- greedy decoder
 struct srq_decoder {
     srq_exec *e = nullptr;
     srq_model *m = nullptr;

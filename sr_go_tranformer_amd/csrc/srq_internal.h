@@ -138,6 +138,25 @@ int launch_advance(hipStream_t s, int32_t *pos, const int32_t *token, int32_t *o
 int launch_row_plan(hipStream_t s, const RowMeta &meta, int32_t n, int32_t kvdim, int32_t head_dim,
                     const float *cos_t, const float *sin_t, int64_t *kvoff, float *rope_cs);
 
+// -------------------------------------------------------------- sampling
+struct SampleArgs {
+    const float *logits;         // [rows x vocab]
+    int32_t rows, vocab;
+    double temperature;          // 0: greedy
+    int32_t top_k;               // 0: off
+    double top_p;                // >= 1: off
+    double repeat_penalty;       // 1: off
+    const int32_t *history;      // [rows x history_stride] or null
+    const int32_t *history_len;  // [rows] or null
+    int32_t history_stride;
+    const int32_t *blocked;      // [rows] (-1: none) or null
+    uint64_t *rng;               // [rows] SplitMix64 states, advanced per draw
+    int32_t *ids;                // [rows] out
+    int32_t *err;                // |= 1 non-finite logit, 2 no candidate, 4/8 selection limits
+};
+int launch_sample(hipStream_t s, const SampleArgs &a, void *scratch);
+size_t sample_scratch_bytes(int32_t rows, int32_t vocab);
+
 // ------------------------------------------------------------- attention
 struct AttnArgs {
     const float *q;     // [n x heads*head_dim]
