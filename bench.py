@@ -344,6 +344,105 @@ def bench_q4mixed_prefill(srq, args):
     return 0
 
 
+def schedule_tokens(remaining, decoding, budget, chunk, mixed_chunk, start):
+    """scheduleTokens (M:8180-8210): one row per active session, then extra
+    prefill rows round-robin from `start` up to min(chunk, remaining) each
+    (chunk capped at mixed_chunk while any session decodes) within `budget`."""
+    n = len(remaining)
+    if any(decoding):
+        chunk = min(chunk, mixed_chunk)
+    counts = [1] * n
+    total = n
+    while total < budget:
+        progress = False
+        for j in range(n):
+            i = (start + j) % n
+            if counts[i] < min(chunk, remaining[i]):
+                counts[i] += 1
+                total += 1
+                progress = True
+                if total == budget:
+                    break
+        if not progress:
+            break
+    return counts
+
+
+def bench_continuous_batching(srq, args):
+    """Llama-3.2-3B shape (3072 / 28 layers / 24:8 heads / 8192 / 128256
+    tied), Q8, seeded N(0, 0.02) weights: 32 concurrent requests, prompt
+    lengths uniform in [64, 1024], 128 output tokens each, paged KV, the
+    reference's scheduling defaults (prefill chunk 16, mixed chunk 1, token
+    budget 64), sampling at temperature 0.8, top-p 0.9, top-k off, no repeat
+    penalty, RNG{seed + i} per request; logits stay on the device."""
+    from sr_go_tranformer_amd import synthetic
+    sessions_n, out_n, budget, chunk, mixed = 32, args.gen_tokens_cb, 64, 16, 1
+    r = synthetic.SplitMix64(args.seed)
+    lens = [64 + r.intn(1024 - 64 + 1) for _ in range(sessions_n)]
+    ex = srq.Executor(0)
+    cfg = synthetic.shape_config("llama3.2-3b", max(lens) + out_n + 1)
+    model = synthetic.build(ex, cfg, "q8", args.seed)
+    prompts = [synthetic.random_prompt(n, cfg.vocab, args.seed * 7 + i) for i, n in enumerate(lens)]
+    pages = sum((n + out_n + 31) // 32 for n in lens)
+    pool = model.pool(pages + 8)
+    caches = [pool.cache((n + out_n + 31) // 32) for n in lens]
+    cursor = [0] * sessions_n
+    outputs = [[] for _ in range(sessions_n)]
+    rng = np.array([(args.seed + i) & ((1 << 64) - 1) for i in range(sessions_n)], np.uint64)
+    params = srq.Sampling(0.8, 0, 0.9, 1.0)
+    active = list(range(sessions_n))
+    steps, rows_total, start = 0, 0, 0
+    ex.synchronize()
+    t0 = time.perf_counter()
+    while active:
+        remaining = [len(prompts[i]) - cursor[i] for i in active]
+        decoding = [rem == 0 for rem in remaining]
+        counts = schedule_tokens(remaining, decoding, budget, chunk, mixed, start)
+        start += 1
+        chunks, want = [], []
+        for k, i in enumerate(active):
+            if decoding[k]:
+                chunks.append([outputs[i][-1]])
+                want.append(True)
+            else:
+                c = counts[k]
+                chunks.append(prompts[i][cursor[i]:cursor[i] + c])
+                want.append(cursor[i] + c == len(prompts[i]))
+        dev = model.step([caches[i] for i in active], chunks, want=want, host=False)
+        rows_total += sum(len(c) for c in chunks)
+        steps += 1
+        sel = [k for k in range(len(active)) if want[k]]
+        if sel:
+            # the step's logits are [sessions x vocab] with unselected rows
+            # zeroed; sample every row and keep the selected ones
+            st = rng[active].copy()
+            ids = srq.sample(ex, dev, len(active), cfg.vocab, params, st)
+            for k in sel:
+                i = active[k]
+                rng[i] = st[k]
+                outputs[i].append(int(ids[k]))
+        for k, i in enumerate(active):
+            if not decoding[k]:
+                cursor[i] += len(chunks[k])
+        done = [i for i in active if len(outputs[i]) >= out_n]
+        for i in done:
+            caches[i].close()
+        active = [i for i in active if len(outputs[i]) < out_n]
+    ex.synchronize()
+    dt = time.perf_counter() - t0
+    gen = sum(len(o) for o in outputs)
+    print(json.dumps({
+        "metric": "Llama-3.2-3B-shape Q8 continuous batching output tokens/s (32 requests)",
+        "value": round(gen / dt, 1), "unit": "tokens/s", "n_gpus": 1, "higher_is_better": True, "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": "Llama-3.2-3B shape, Q8, 32 requests, prompts U[64,1024], %d outputs each, "
+                               "budget 64 / chunk 16 / mixed 1, T 0.8 top-p 0.9" % out_n, "seed": args.seed},
+        "seconds": round(dt, 3), "steps": steps, "rows_processed": rows_total,
+        "rows_per_s": round(rows_total / dt, 1), "ms_per_step": round(dt * 1e3 / steps, 3),
+        "prompt_tokens": sum(lens), "generated_tokens": gen}), flush=True)
+    return 0
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -355,10 +454,12 @@ def main():
     ap.add_argument("--gemv-launches", type=int, default=320)
     ap.add_argument("--config", default="mistral7b-q8-decode",
                     choices=["mistral7b-q8-decode", "smollm2-q8-decode", "llama1b-q8-gemv-sweep",
-                             "mistral7b-q4mixed-prefill"],
+                             "mistral7b-q4mixed-prefill", "llama3b-q8-continuous-batching"],
                     help="workload; the default is the headline Mistral-7B Q8 decode")
     ap.add_argument("--prompt-tokens", type=int, default=2048, help="mistral7b-q4mixed-prefill: prompt length")
     ap.add_argument("--gen-tokens", type=int, default=128, help="mistral7b-q4mixed-prefill: generated tokens")
+    ap.add_argument("--gen-tokens-cb", type=int, default=128,
+                    help="llama3b-q8-continuous-batching: output tokens per request")
     ap.add_argument("--gemv-only", action="store_true",
                     help="run only the GEMV roofline leg (standalone weights) and a calibration copy")
     ap.add_argument("--gemv-rows", type=int, default=28672, help="--gemv-only: weight rows (4096 columns)")
@@ -385,6 +486,8 @@ def main():
         return bench_gemv_sweep(srq, args)
     if args.config == "mistral7b-q4mixed-prefill":
         return bench_q4mixed_prefill(srq, args)
+    if args.config == "llama3b-q8-continuous-batching":
+        return bench_continuous_batching(srq, args)
 
     t_start = time.perf_counter()
     ex = srq.Executor(0)

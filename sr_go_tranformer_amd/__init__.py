@@ -350,20 +350,23 @@ class Model:
     def pool(self, max_pages):
         return Pool(self, max_pages)
 
-    def step(self, caches, chunks, want=None, cancel=None):
-        """prefillSelected: returns host logits [sessions, vocab]."""
+    def step(self, caches, chunks, want=None, cancel=None, host=True):
+        """prefillSelected: returns host logits [sessions, vocab], or with
+        host=False the device pointer of the step's logits (borrowed until
+        the executor's next step)."""
         sessions = len(caches)
         lens = np.array([len(c) for c in chunks], np.int32)
         tokens = np.concatenate([np.asarray(c, np.int32) for c in chunks]).astype(np.int32)
         handles = (C.c_void_p * sessions)(*[c.h for c in caches])
         w = None if want is None else np.array(want, np.uint8)
-        out = np.zeros((sessions, self.config.vocab), np.float32)
+        out = np.zeros((sessions, self.config.vocab), np.float32) if host else None
         dev = C.c_void_p()
         cflag = None if cancel is None else C.cast(C.pointer(cancel), C.c_void_p)
         check(lib().srq_step(self.ex.h, self.h, sessions, C.cast(handles, C.c_void_p), _np_ptr(lens), _np_ptr(tokens),
-                             _np_ptr(w) if w is not None else None, C.byref(dev), _np_ptr(out), cflag))
+                             _np_ptr(w) if w is not None else None, C.byref(dev),
+                             _np_ptr(out) if host else None, cflag))
         self.last_logits_ptr = dev.value
-        return out
+        return out if host else dev
 
     def argmax_last(self, rows=1):
         ids = np.zeros(rows, np.int32)

@@ -295,7 +295,72 @@ __global__ __launch_bounds__(kST) void sample_kernel(const SampleArgs A, unsigne
                 continue;
             }
             if (n > (uint32_t)kList) {
-                if (tid == 0) atomicOr(A.err, 4);  // more equal-ranked candidates than one sort holds
+                // More candidates than one sort holds.  If they all hold one
+                // value their order is by id alone: take the m-th smallest id.
+                double bmn = DBL_MAX, bmx = -DBL_MAX;
+                unsigned long long pe = 0;
+                for (int i = tid; i < vocab; i += kST) {
+                    const double v = value(i, lg[i]);
+                    if (!member(i, v) || !inside(v) || bucket_of(v, lo, scale) != b) continue;
+                    bmn = fmin(bmn, v), bmx = fmax(bmx, v), pe = P[i];
+                }
+                bmn = block_min(bmn, s);
+                bmx = block_max(bmx, s);
+                for (int o = 32; o > 0; o >>= 1) pe = max(pe, (unsigned long long)__shfl_xor(pe, o, 64));
+                if ((tid & 63) == 0) s.red_u[tid >> 6] = pe;
+                __syncthreads();
+                pe = 0;
+                for (int w = 0; w < kST / 64; ++w) pe = max(pe, s.red_u[w]);
+                __syncthreads();
+                const unsigned long long need = target - above;  // > 0: the cut lies in this bucket
+                if (bmn != bmx || (mode != CUT_COUNT && pe == 0)) {
+                    if (tid == 0) atomicOr(A.err, 4);
+                    return;
+                }
+                const unsigned long long m = mode == CUT_COUNT    ? need
+                                             : mode == CUT_MASS_GE ? (need + pe - 1) / pe
+                                                                   : need / pe + 1;
+                const int width = (vocab + kBuckets - 1) / kBuckets;  // ids per id bucket
+                for (int k = tid; k < kBuckets; k += kST) s.hcount[k] = 0;
+                __syncthreads();
+                for (int i = tid; i < vocab; i += kST) {
+                    const double v = value(i, lg[i]);
+                    if (member(i, v) && inside(v) && bucket_of(v, lo, scale) == b) atomicAdd(&s.hcount[i / width], 1u);
+                }
+                __syncthreads();
+                if (tid == 0) {
+                    unsigned long long c = 0;
+                    int k = 0;
+                    for (; k < kBuckets; ++k) {
+                        if (c + s.hcount[k] >= m) break;
+                        c += s.hcount[k];
+                    }
+                    s.bucket = k;
+                    s.above = c;  // candidates of lower ids
+                    s.list_n = 0;
+                }
+                __syncthreads();
+                const int ib = s.bucket;
+                for (int i = ib * width + tid; i < min(vocab, (ib + 1) * width); i += kST) {
+                    const double v = value(i, lg[i]);
+                    if (member(i, v) && inside(v) && bucket_of(v, lo, scale) == b) s.li[atomicAdd(&s.list_n, 1)] = i;
+                }
+                __syncthreads();
+                if (tid == 0) {
+                    // the (m - above)-th smallest gathered id (at most `width` of them)
+                    const int want = (int)(m - s.above) - 1, ln = s.list_n;
+                    for (int a = 0; a <= want; ++a) {
+                        int mn = a;
+                        for (int c2 = a + 1; c2 < ln; ++c2)
+                            if (s.li[c2] < s.li[mn]) mn = c2;
+                        const int t2 = s.li[a];
+                        s.li[a] = s.li[mn], s.li[mn] = t2;
+                    }
+                    s.cut = Cand{bmn, s.li[want]};
+                    s.cum = above + (mode == CUT_COUNT ? m : m * pe);
+                    s.found = 1;
+                }
+                __syncthreads();
                 return;
             }
             // Gather the bucket's candidates, sort them in order, scan.

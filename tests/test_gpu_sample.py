@@ -126,3 +126,21 @@ def test_sample_errors(ex):
     # the executor stays usable: greedy over a clean row
     ids, _ = run(ex, np.array([[0.0, 3.0, 3.0]], np.float32), srq.Sampling(0.0, 0, 1.0, 1.0), [5])
     assert list(ids) == [1]
+
+
+def test_sample_flat_rows_rank_by_id(ex):
+    """Rows holding one value (e.g. the zeroed rows of unselected sessions)
+    and a run of 10^4 equal values at the nucleus edge: the candidates past
+    one bucket's sort are ranked by id."""
+    rng = np.random.default_rng(11)
+    vocab = 128256
+    logits = np.zeros((4, vocab), np.float32)
+    logits[2, :] = -3.0
+    logits[3, :] = rng.normal(0, 1.0, size=vocab).astype(np.float32)
+    logits[3, 1000:11000] = 0.5
+    seeds = rng.integers(0, 2**63, size=4, dtype=np.uint64)
+    for t, k, p in [(0.8, 0, 0.9), (0.8, 0, 1.0), (1.0, 50000, 1.0), (0.5, 3000, 0.7)]:
+        got, gst = run(ex, logits, srq.Sampling(t, k, p, 1.0), seeds)
+        want, wst = oracle_rows(logits, t, k, p, 1.0, seeds)
+        assert np.array_equal(got, want), (t, k, p, got, want)
+        assert np.array_equal(gst, wst)
