@@ -284,11 +284,9 @@ RowMeta make_meta(srq_exec *e, srq_model *m, int layer, int32_t pt_stride, const
 int run_linear(srq_exec *e, Workspace &ws, const srq_weight &w, const float *x, int32_t n, float *y, int64_t y_stride,
                const float *norm_w, double eps, const float *residual) {
     if (n > 16 && gemm_ok(w.fmt, w.cols) && !norm_w) {
-        SRQ_CHECK(ensure(ws.flags, sizeof(int32_t) * (size_t)n, e->stream));
-        SRQ_CHECK(launch_wide_scan(e->stream, x, n, w.cols, as<int32_t>(ws.flags)));
+        SRQ_CHECK(ensure(ws.flags, gemm_scratch_bytes(n, w.rows, w.cols), e->stream));
         GemmArgs g{w.fmt, w.values, w.scales, w.rows, w.cols, x, n, y, y_stride, residual};
-        SRQ_CHECK(launch_gemm(e->stream, g, as<int32_t>(ws.flags)));
-        return launch_wide_fix(e->stream, g, as<int32_t>(ws.flags));
+        return launch_gemm(e->stream, g, ws.flags.p, ws.flags.n);
     }
     const int nb = gemv_max_rows(w.fmt, w.cols, norm_w != nullptr, 0);
     if (nb < 1) return fail(SRQ_EINVAL, "input width %lld exceeds the GEMV staging limit", (long long)w.cols);

@@ -2,12 +2,13 @@
 //
 // Counterpart of linearQ8Into / linearQ4Into / linearFP32Range
 // (cmd/monolith/monolith.go M:3942-4780) when many activation rows share
-// each weight read, which makes the contraction compute bound.
+// each weight read.
 //
-// Tiling (gfx950, wave64, v_mfma_f32_16x16x4_f32):
-//  - Workgroup tile 64 (activation rows) x 128 (output features), K step 32
-//    (half a scale block).  4 waves in a 2x2 grid, each owning 32x64 = 2x4
-//    MFMA tiles of 16x16 with FP32 accumulators.
+// Tiling (gfx950, wave64, v_mfma_f32_16x16x4f32):
+//  - Workgroup tile BMT (activation rows: 32 when n <= 32, else 64) x 128
+//    (output features), K step 32 (half a scale block).  4 waves; each owns
+//    32 rows x (128 / waves across N) features as 16x16 MFMA tiles with FP32
+//    accumulators.
 //  - Weights are read once per K step as int8 / packed int4 / f32,
 //    dequantised in registers to f32(code)*scale (the copyRow rounding,
 //    M:3900-3921) and stored to LDS; activations go to LDS unchanged.
@@ -15,14 +16,25 @@
 //    8g+s, so every lane reads its 8 K values of a row as two ds_read_b128.
 //  - Global loads for step k+1 are issued before the MFMAs of step k
 //    (register double buffering); LDS is double buffered.
-//  - Rows flagged wide (|x| > f32(MaxFloat32/(2*64*127)), M:4346-4354) are
-//    skipped here and recomputed in FP64 by wide_fix_kernel.
+//  - Split K: when the (features x rows) tiles alone cannot fill the chip
+//    (few rows per step, narrow outputs), blockIdx.z takes a slice of the
+//    K steps and writes its partial sums to scratch; gemm_reduce_kernel adds
+//    the slices in slice order, then the residual.  Results are
+//    deterministic for a given (n, rows, cols).
+//  - Rows holding any |x| > f32(MaxFloat32/(2*64*127)) (M:4346-4354) are
+//    detected while staging x and recomputed in FP64 (linearQ8WideInto /
+//    linearQ4WideInto, M:4356-4382, M:4754-4780): by the workgroup itself
+//    when it saw all of K, else by the reduction from per-slice flags.
+#include <algorithm>
+
 #include "srq_internal.h"
 
 namespace srq {
 namespace {
 
-constexpr int BM = 64, BN = 128, BK = 32, LDK = BK + 4;
+constexpr int BN = 128, BK = 32, LDK = BK + 4;
+constexpr int kFillWGs = 512;      // two resident workgroups on each of 256 CUs
+constexpr int kMinSliceSteps = 8;  // K steps per split-K slice (256 inputs)
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 template <int FMT>
@@ -85,120 +97,46 @@ __device__ __forceinline__ void store_b(float *Bs, int tid, const uint4 (&raw)[4
     for (int i = 0; i < 4; ++i) *(float4 *)(dst + 4 * i) = make_float4(w[4 * i], w[4 * i + 1], w[4 * i + 2], w[4 * i + 3]);
 }
 
+// Activation tile BMT x BK: each thread stages BMT*BK/256 floats of one row.
+template <int BMT>
+struct ATile {
+    static constexpr int FPT = BMT * BK / 256;  // floats per thread (8 or 4)
+    static constexpr int TPR = BK / FPT;        // threads per row
+    static constexpr int NV = FPT / 4;          // float4 per thread
+};
+
+template <int BMT>
 __device__ __forceinline__ void load_a(const float *__restrict__ X, int32_t n, int64_t cols, int64_t m0, int64_t k0,
-                                       int tid, float4 (&a)[2]) {
-    const int r = tid >> 2, kq = (tid & 3) * 8;
+                                       int tid, float4 (&a)[ATile<BMT>::NV]) {
+    constexpr int FPT = ATile<BMT>::FPT, TPR = ATile<BMT>::TPR, NV = ATile<BMT>::NV;
+    const int r = tid / TPR, kq = (tid % TPR) * FPT;
     const int64_t m = m0 + r;
     if (m < n) {
         const float4 *p = (const float4 *)(X + m * cols + k0 + kq);
-        a[0] = p[0];
-        a[1] = p[1];
+#pragma unroll
+        for (int i = 0; i < NV; ++i) a[i] = p[i];
     } else {
-        a[0] = a[1] = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int i = 0; i < NV; ++i) a[i] = make_float4(0.f, 0.f, 0.f, 0.f);
     }
 }
 
-__device__ __forceinline__ void store_a(float *As, int tid, const float4 (&a)[2]) {
-    const int r = tid >> 2, kq = (tid & 3) * 8;
-    *(float4 *)(As + r * LDK + kq) = a[0];
-    *(float4 *)(As + r * LDK + kq + 4) = a[1];
-}
-
-template <int FMT>
-__global__ __launch_bounds__(256) void gemm_kernel(const GemmArgs G, const int32_t *__restrict__ wide) {
-    __shared__ __attribute__((aligned(16))) float As[2][BM * LDK];
-    __shared__ __attribute__((aligned(16))) float Bs[2][BN * LDK];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
-    const int64_t n0 = (int64_t)blockIdx.x * BN, m0 = (int64_t)blockIdx.y * BM;
-    const uint8_t *W = (const uint8_t *)G.values;
-    const int64_t cols = G.cols;
-    const int ksteps = (int)(cols / BK);
-
-    floatx4 acc[2][4];
+// Stores the staged floats; returns the largest |x| among them.
+template <int BMT>
+__device__ __forceinline__ float store_a(float *As, int tid, const float4 (&a)[ATile<BMT>::NV]) {
+    constexpr int FPT = ATile<BMT>::FPT, TPR = ATile<BMT>::TPR, NV = ATile<BMT>::NV;
+    const int r = tid / TPR, kq = (tid % TPR) * FPT;
+    float amax = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
-
-    uint4 braw[4];
-    float bscale;
-    float4 areg[2];
-    load_b<FMT>(W, G.scales, G.rows, cols, n0, 0, tid, braw, bscale);
-    load_a(G.x, G.n, cols, m0, 0, tid, areg);
-    store_b<FMT>(Bs[0], tid, braw, bscale);
-    store_a(As[0], tid, areg);
-    __syncthreads();
-
-    const int gq = lane >> 4, li = lane & 15;
-    for (int ks = 0; ks < ksteps; ++ks) {
-        const int cur = ks & 1;
-        if (ks + 1 < ksteps) {
-            load_b<FMT>(W, G.scales, G.rows, cols, n0, (int64_t)(ks + 1) * BK, tid, braw, bscale);
-            load_a(G.x, G.n, cols, m0, (int64_t)(ks + 1) * BK, tid, areg);
-        }
-        const float *as = As[cur], *bs = Bs[cur];
-        float af[2][8], bf[4][8];
-#pragma unroll
-        for (int tm = 0; tm < 2; ++tm) {
-            const float *p = as + (wm * 32 + tm * 16 + li) * LDK + 8 * gq;
-            const float4 u = *(const float4 *)p, v = *(const float4 *)(p + 4);
-            af[tm][0] = u.x, af[tm][1] = u.y, af[tm][2] = u.z, af[tm][3] = u.w;
-            af[tm][4] = v.x, af[tm][5] = v.y, af[tm][6] = v.z, af[tm][7] = v.w;
-        }
-#pragma unroll
-        for (int tn = 0; tn < 4; ++tn) {
-            const float *p = bs + (wn * 64 + tn * 16 + li) * LDK + 8 * gq;
-            const float4 u = *(const float4 *)p, v = *(const float4 *)(p + 4);
-            bf[tn][0] = u.x, bf[tn][1] = u.y, bf[tn][2] = u.z, bf[tn][3] = u.w;
-            bf[tn][4] = v.x, bf[tn][5] = v.y, bf[tn][6] = v.z, bf[tn][7] = v.w;
-        }
-#pragma unroll
-        for (int s = 0; s < 8; ++s)
-#pragma unroll
-            for (int tm = 0; tm < 2; ++tm)
-#pragma unroll
-                for (int tn = 0; tn < 4; ++tn)
-                    acc[tm][tn] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[tm][s], bf[tn][s], acc[tm][tn], 0, 0, 0);
-        if (ks + 1 < ksteps) {
-            store_b<FMT>(Bs[cur ^ 1], tid, braw, bscale);
-            store_a(As[cur ^ 1], tid, areg);
-        }
-        __syncthreads();
+    for (int i = 0; i < NV; ++i) {
+        *(float4 *)(As + r * LDK + kq + 4 * i) = a[i];
+        amax = fmaxf(amax, fmaxf(fmaxf(fabsf(a[i].x), fabsf(a[i].y)), fmaxf(fabsf(a[i].z), fabsf(a[i].w))));
     }
-
-    // D layout of 16x16x4: lane holds rows 4*(lane/16)+r, column lane%16.
-#pragma unroll
-    for (int tm = 0; tm < 2; ++tm)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int64_t m = m0 + wm * 32 + tm * 16 + 4 * gq + r;
-            if (m >= G.n || (wide && wide[m])) continue;
-#pragma unroll
-            for (int tn = 0; tn < 4; ++tn) {
-                const int64_t j = n0 + wn * 64 + tn * 16 + li;
-                if (j >= G.rows) continue;
-                float v = acc[tm][tn][r];
-                if (G.residual) v = G.residual[m * G.y_stride + j] + v;
-                G.y[m * G.y_stride + j] = v;
-            }
-        }
+    return amax;
 }
 
-__global__ __launch_bounds__(256) void wide_scan_kernel(const float *__restrict__ x, int64_t cols,
-                                                        int32_t *__restrict__ flags) {
-    __shared__ int any;
-    if (threadIdx.x == 0) any = 0;
-    __syncthreads();
-    const float *xr = x + (int64_t)blockIdx.x * cols;
-    int w = 0;
-    for (int64_t c = threadIdx.x; c < cols; c += 256) w |= fabsf(xr[c]) > kWideLimit;
-    if (w) any = 1;
-    __syncthreads();
-    if (threadIdx.x == 0) flags[blockIdx.x] = any;
-}
-
-// linearQ8WideInto / linearQ4WideInto (M:4356-4382, M:4754-4780).
+// linearQ8WideInto / linearQ4WideInto (M:4356-4382, M:4754-4780): output o
+// of row m in FP64, per-block partial sums scaled in FP64, plus residual.
 __device__ __forceinline__ double wide_weight(int fmt, const uint8_t *wrow, int64_t c) {
     if (fmt == SRQ_Q8) return (double)((const int8_t *)wrow)[c];
     if (fmt == SRQ_Q4) {
@@ -209,11 +147,7 @@ __device__ __forceinline__ double wide_weight(int fmt, const uint8_t *wrow, int6
     return (double)((const float *)wrow)[c];
 }
 
-__global__ __launch_bounds__(256) void wide_fix_kernel(const GemmArgs G, const int32_t *__restrict__ flags) {
-    const int64_t m = blockIdx.y;
-    if (!flags[m]) return;
-    const int64_t o = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (o >= G.rows) return;
+__device__ __forceinline__ float wide_output(const GemmArgs &G, int64_t m, int64_t o) {
     const uint8_t *wrow = (const uint8_t *)G.values + o * row_bytes(G.fmt, G.cols);
     const float *xr = G.x + m * G.cols;
     const int64_t groups = groups_of(G.cols);
@@ -226,7 +160,180 @@ __global__ __launch_bounds__(256) void wide_fix_kernel(const GemmArgs G, const i
     }
     float v = (float)sum;
     if (G.residual) v = G.residual[m * G.y_stride + o] + v;
-    G.y[m * G.y_stride + o] = v;
+    return v;
+}
+
+// partial == nullptr: one slice covers all K and the tile writes y.
+// Otherwise slice blockIdx.z covers K steps [z*kper, (z+1)*kper) and
+// writes partial[z][m][j] (n x rows per slice) and, from the first feature
+// tile, wflags[z][m].
+template <int FMT, int BMT>
+__global__ __launch_bounds__(256) void gemm_kernel(const GemmArgs G, float *__restrict__ partial,
+                                                   int32_t *__restrict__ wflags, const int kper) {
+    constexpr int WM = BMT / 32, WN = 4 / WM, TN = BN / WN / 16, NV = ATile<BMT>::NV;
+    __shared__ __attribute__((aligned(16))) float As[2][BMT * LDK];
+    __shared__ __attribute__((aligned(16))) float Bs[2][BN * LDK];
+    __shared__ int row_wide[BMT];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave / WN, wn = wave % WN;
+    const int64_t n0 = (int64_t)blockIdx.x * BN, m0 = (int64_t)blockIdx.y * BMT;
+    const uint8_t *W = (const uint8_t *)G.values;
+    const int64_t cols = G.cols;
+    const int kbeg = (int)blockIdx.z * kper;
+    const int kend = min(kbeg + kper, (int)(cols / BK));
+    if (tid < BMT) row_wide[tid] = 0;
+
+    floatx4 acc[2][TN];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+    uint4 braw[4];
+    float bscale;
+    float4 areg[NV];
+    load_b<FMT>(W, G.scales, G.rows, cols, n0, (int64_t)kbeg * BK, tid, braw, bscale);
+    load_a<BMT>(G.x, G.n, cols, m0, (int64_t)kbeg * BK, tid, areg);
+    store_b<FMT>(Bs[0], tid, braw, bscale);
+    float amax = store_a<BMT>(As[0], tid, areg);
+    __syncthreads();
+
+    const int gq = lane >> 4, li = lane & 15;
+    for (int ks = kbeg; ks < kend; ++ks) {
+        const int cur = (ks - kbeg) & 1;
+        if (ks + 1 < kend) {
+            load_b<FMT>(W, G.scales, G.rows, cols, n0, (int64_t)(ks + 1) * BK, tid, braw, bscale);
+            load_a<BMT>(G.x, G.n, cols, m0, (int64_t)(ks + 1) * BK, tid, areg);
+        }
+        const float *as = As[cur], *bs = Bs[cur];
+        float af[2][8], bf[TN][8];
+#pragma unroll
+        for (int tm = 0; tm < 2; ++tm) {
+            const float *p = as + (wm * 32 + tm * 16 + li) * LDK + 8 * gq;
+            const float4 u = *(const float4 *)p, v = *(const float4 *)(p + 4);
+            af[tm][0] = u.x, af[tm][1] = u.y, af[tm][2] = u.z, af[tm][3] = u.w;
+            af[tm][4] = v.x, af[tm][5] = v.y, af[tm][6] = v.z, af[tm][7] = v.w;
+        }
+#pragma unroll
+        for (int tn = 0; tn < TN; ++tn) {
+            const float *p = bs + (wn * TN * 16 + tn * 16 + li) * LDK + 8 * gq;
+            const float4 u = *(const float4 *)p, v = *(const float4 *)(p + 4);
+            bf[tn][0] = u.x, bf[tn][1] = u.y, bf[tn][2] = u.z, bf[tn][3] = u.w;
+            bf[tn][4] = v.x, bf[tn][5] = v.y, bf[tn][6] = v.z, bf[tn][7] = v.w;
+        }
+#pragma unroll
+        for (int s = 0; s < 8; ++s)
+#pragma unroll
+            for (int tm = 0; tm < 2; ++tm)
+#pragma unroll
+                for (int tn = 0; tn < TN; ++tn)
+                    acc[tm][tn] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[tm][s], bf[tn][s], acc[tm][tn], 0, 0, 0);
+        if (ks + 1 < kend) {
+            store_b<FMT>(Bs[cur ^ 1], tid, braw, bscale);
+            amax = fmaxf(amax, store_a<BMT>(As[cur ^ 1], tid, areg));
+        }
+        __syncthreads();
+    }
+    if (amax > kWideLimit) row_wide[tid / ATile<BMT>::TPR] = 1;
+    __syncthreads();
+
+    // D layout of 16x16x4: lane holds rows 4*(lane/16)+r, column lane%16.
+    if (partial) {
+        float *P = partial + (int64_t)blockIdx.z * G.n * G.rows;
+        if (blockIdx.x == 0 && tid < BMT && m0 + tid < G.n) wflags[(int64_t)blockIdx.z * G.n + m0 + tid] = row_wide[tid];
+#pragma unroll
+        for (int tm = 0; tm < 2; ++tm)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int64_t m = m0 + wm * 32 + tm * 16 + 4 * gq + r;
+                if (m >= G.n) continue;
+#pragma unroll
+                for (int tn = 0; tn < TN; ++tn) {
+                    const int64_t j = n0 + wn * TN * 16 + tn * 16 + li;
+                    if (j < G.rows) P[m * G.rows + j] = acc[tm][tn][r];
+                }
+            }
+        return;
+    }
+#pragma unroll
+    for (int tm = 0; tm < 2; ++tm)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int mi = wm * 32 + tm * 16 + 4 * gq + r;
+            const int64_t m = m0 + mi;
+            if (m >= G.n || row_wide[mi]) continue;
+#pragma unroll
+            for (int tn = 0; tn < TN; ++tn) {
+                const int64_t j = n0 + wn * TN * 16 + tn * 16 + li;
+                if (j >= G.rows) continue;
+                float v = acc[tm][tn][r];
+                if (G.residual) v = G.residual[m * G.y_stride + j] + v;
+                G.y[m * G.y_stride + j] = v;
+            }
+        }
+    // This workgroup saw all of K: it recomputes its wide rows itself.
+    for (int mi = 0; mi < BMT; ++mi) {
+        if (!row_wide[mi] || m0 + mi >= G.n) continue;
+        const int64_t j = n0 + tid;
+        if (tid < BN && j < G.rows) G.y[(m0 + mi) * G.y_stride + j] = wide_output(G, m0 + mi, j);
+    }
+}
+
+// y[m][j] = residual + sum over slices z (in order) of partial[z][m][j];
+// rows flagged wide by any slice take the FP64 path instead.
+__global__ __launch_bounds__(256) void gemm_reduce_kernel(const GemmArgs G, const float *__restrict__ partial,
+                                                          const int32_t *__restrict__ wflags, const int slices) {
+    const int64_t m = blockIdx.y, j = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    int wide = 0;
+    for (int z = 0; z < slices; ++z) wide |= wflags[(int64_t)z * G.n + m];
+    if (j >= G.rows) return;
+    float v;
+    if (wide) {
+        v = wide_output(G, m, j);
+    } else {
+        const int64_t plane = (int64_t)G.n * G.rows;
+        const float *p = partial + m * G.rows + j;
+        float s = p[0];
+        for (int z = 1; z < slices; ++z) s += p[z * plane];
+        v = G.residual ? G.residual[m * G.y_stride + j] + s : s;
+    }
+    G.y[m * G.y_stride + j] = v;
+}
+
+struct GemmPlan {
+    int bm, slices, kper;
+};
+
+// Tile height from n; K slices so that tiles x slices reach kFillWGs
+// workgroups, each slice at least kMinSliceSteps K steps.
+GemmPlan plan_gemm(int32_t n, int64_t rows, int64_t cols) {
+    GemmPlan p;
+    p.bm = n <= 32 ? 32 : 64;
+    const int64_t tiles = ((rows + BN - 1) / BN) * ((n + p.bm - 1) / p.bm);
+    const int ksteps = (int)(cols / BK);
+    int slices = 1;
+    if (tiles < kFillWGs) {
+        const int64_t want = (kFillWGs + tiles - 1) / tiles;
+        slices = (int)std::max<int64_t>(1, std::min<int64_t>(want, ksteps / kMinSliceSteps));
+    }
+    p.kper = (ksteps + slices - 1) / slices;
+    p.slices = (ksteps + p.kper - 1) / p.kper;
+    return p;
+}
+
+template <int FMT, int BMT>
+void launch_tiles(hipStream_t s, const GemmArgs &a, const GemmPlan &p, float *partial, int32_t *wflags) {
+    dim3 grid((unsigned)((a.rows + BN - 1) / BN), (unsigned)((a.n + BMT - 1) / BMT), (unsigned)p.slices);
+    gemm_kernel<FMT, BMT><<<grid, 256, 0, s>>>(a, partial, wflags, p.kper);
+}
+
+template <int BMT>
+void launch_fmt(hipStream_t s, const GemmArgs &a, const GemmPlan &p, float *partial, int32_t *wflags) {
+    switch (a.fmt) {
+        case SRQ_Q8: launch_tiles<SRQ_Q8, BMT>(s, a, p, partial, wflags); break;
+        case SRQ_Q4: launch_tiles<SRQ_Q4, BMT>(s, a, p, partial, wflags); break;
+        default: launch_tiles<SRQ_F32, BMT>(s, a, p, partial, wflags); break;
+    }
 }
 
 }  // namespace
@@ -236,31 +343,36 @@ bool gemm_ok(int fmt, int64_t cols) {
     return cols % BK == 0 && cols >= BK;
 }
 
-int launch_gemm(hipStream_t s, const GemmArgs &a, const int32_t *wide) {
+size_t gemm_scratch_bytes(int32_t n, int64_t rows, int64_t cols) {
+    if (n <= 0 || rows <= 0 || !gemm_ok(SRQ_F32, cols)) return 0;
+    const GemmPlan p = plan_gemm(n, rows, cols);
+    if (p.slices == 1) return 0;
+    return (size_t)p.slices * (size_t)n * ((size_t)rows + 1) * 4;
+}
+
+int launch_gemm(hipStream_t s, const GemmArgs &a, void *scratch, size_t scratch_bytes) {
     if (a.n <= 0 || a.rows <= 0) return SRQ_OK;
     if (!gemm_ok(a.fmt, a.cols)) return fail(SRQ_EINVAL, "gemm: cols=%lld not a multiple of %d", (long long)a.cols, BK);
-    dim3 grid((unsigned)((a.rows + BN - 1) / BN), (unsigned)((a.n + BM - 1) / BM));
-    switch (a.fmt) {
-        case SRQ_Q8: gemm_kernel<SRQ_Q8><<<grid, 256, 0, s>>>(a, wide); break;
-        case SRQ_Q4: gemm_kernel<SRQ_Q4><<<grid, 256, 0, s>>>(a, wide); break;
-        default: gemm_kernel<SRQ_F32><<<grid, 256, 0, s>>>(a, wide); break;
+    const GemmPlan p = plan_gemm(a.n, a.rows, a.cols);
+    float *partial = nullptr;
+    int32_t *wflags = nullptr;
+    if (p.slices > 1) {
+        const size_t need = gemm_scratch_bytes(a.n, a.rows, a.cols);
+        if (!scratch || scratch_bytes < need)
+            return fail(SRQ_EINVAL, "gemm: scratch of %zu bytes, %zu needed", scratch_bytes, need);
+        partial = (float *)scratch;
+        wflags = (int32_t *)(partial + (size_t)p.slices * a.n * a.rows);
     }
+    if (p.bm == 32)
+        launch_fmt<32>(s, a, p, partial, wflags);
+    else
+        launch_fmt<64>(s, a, p, partial, wflags);
     SRQ_HIP(hipGetLastError());
-    return SRQ_OK;
-}
-
-int launch_wide_scan(hipStream_t s, const float *x, int32_t n, int64_t cols, int32_t *flags) {
-    if (n <= 0) return SRQ_OK;
-    wide_scan_kernel<<<n, 256, 0, s>>>(x, cols, flags);
-    SRQ_HIP(hipGetLastError());
-    return SRQ_OK;
-}
-
-int launch_wide_fix(hipStream_t s, const GemmArgs &a, const int32_t *flags) {
-    if (a.n <= 0 || a.rows <= 0) return SRQ_OK;
-    dim3 grid((unsigned)((a.rows + 255) / 256), (unsigned)a.n);
-    wide_fix_kernel<<<grid, 256, 0, s>>>(a, flags);
-    SRQ_HIP(hipGetLastError());
+    if (p.slices > 1) {
+        dim3 grid((unsigned)((a.rows + 255) / 256), (unsigned)a.n);
+        gemm_reduce_kernel<<<grid, 256, 0, s>>>(a, partial, wflags, p.slices);
+        SRQ_HIP(hipGetLastError());
+    }
     return SRQ_OK;
 }
 

@@ -116,13 +116,12 @@ struct GemmArgs {
     int64_t y_stride;
     const float *residual;  // y = residual + acc when non-null (may alias y)
 };
-// wide: per-row flags from launch_wide_scan (rows set are left to wide_fix).
-int launch_gemm(hipStream_t s, const GemmArgs &a, const int32_t *wide);
+// y = x . W^T (+ residual) on MFMA.  Rows holding a wide |x| are computed
+// in FP64.  scratch: gemm_scratch_bytes(n, rows, cols) bytes of device
+// memory for split-K partial sums (0: none needed).
+int launch_gemm(hipStream_t s, const GemmArgs &a, void *scratch, size_t scratch_bytes);
+size_t gemm_scratch_bytes(int32_t n, int64_t rows, int64_t cols);
 bool gemm_ok(int fmt, int64_t cols);
-// Per-row wide flags of x [n x cols] (1 if any |x| > kWideLimit) and the
-// FP64 recomputation of flagged rows.
-int launch_wide_scan(hipStream_t s, const float *x, int32_t n, int64_t cols, int32_t *flags);
-int launch_wide_fix(hipStream_t s, const GemmArgs &a, const int32_t *flags);
 
 // ------------------------------------------------------------------ glue
 int launch_rmsnorm(hipStream_t s, const float *x, const float *w, float *y, int32_t n, int32_t d, double eps);

@@ -193,11 +193,14 @@ def test_linear_gemv_shapes(ex, fmt, shape, n):
 
 
 @pytest.mark.parametrize("fmt", [srq.Q8, srq.Q4, srq.F32])
-@pytest.mark.parametrize("n", [17, 64, 100, 256])
-def test_linear_gemm_mfma(ex, fmt, n):
-    print("gemm", fmt, n, flush=True)
-    rows, cols = 640, 2048
-    rng = oracle.RNG(77 + n)
+@pytest.mark.parametrize("n", [17, 32, 33, 64, 100, 256])
+@pytest.mark.parametrize("shape", [(640, 2048), (1000, 256), (300, 8192)])
+def test_linear_gemm_mfma(ex, fmt, n, shape):
+    """32-row tiles (n <= 32) and 64-row tiles; K split into slices (narrow
+    outputs, long K) and whole-K tiles (K = 256)."""
+    print("gemm", fmt, n, shape, flush=True)
+    rows, cols = shape
+    rng = oracle.RNG(77 + n + cols)
     dense = rng.fill_normal(rows * cols, 0.02).reshape(rows, cols)
     x = rng.fill_normal(n * cols, 1.0).reshape(n, cols)
     w, ow = _weights(ex, dense, fmt)
@@ -209,12 +212,15 @@ def test_linear_gemm_mfma(ex, fmt, n):
     assert np.array_equal(got2.view(np.uint32), got[perm].view(np.uint32))
 
 
-def test_linear_gemm_wide_rows(ex):
-    rows, cols, n = 200, 1024, 40
+@pytest.mark.parametrize("shape", [(200, 1024, 40), (200, 1024, 20), (1000, 256, 40), (1000, 256, 20)])
+def test_linear_gemm_wide_rows(ex, shape):
+    """Wide rows found by split-K slices (K = 1024) and by whole-K tiles
+    (K = 256), with 32- and 64-row tiles."""
+    rows, cols, n = shape
     x, dense = oracle.linear_fixture(n, cols, rows)
     x = x.copy()
     x[3, 5] = FMAX / np.float32(4)
-    x[30, 100] = np.float32(-1e37)
+    x[n - 3, 100] = np.float32(-1e37)
     w, ow = _weights(ex, dense * np.float32(0.001), srq.Q8)
     got = srq.linear(ex, w, x)
     near(got, oracle.linear_closed_f64(ow, x), 2e-5)
