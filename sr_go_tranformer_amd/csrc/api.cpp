@@ -284,7 +284,7 @@ RowMeta make_meta(srq_exec *e, srq_model *m, int layer, int32_t pt_stride, const
 int run_linear(srq_exec *e, Workspace &ws, const srq_weight &w, const float *x, int32_t n, float *y, int64_t y_stride,
                const float *norm_w, double eps, const float *residual) {
     if (n > 16 && gemm_ok(w.fmt, w.cols) && !norm_w) {
-        SRQ_CHECK(ensure(ws.flags, gemm_scratch_bytes(n, w.rows, w.cols), e->stream));
+        SRQ_CHECK(ensure(ws.flags, gemm_scratch_bytes(w.fmt, n, w.rows, w.cols), e->stream));
         GemmArgs g{w.fmt, w.values, w.scales, w.rows, w.cols, x, n, y, y_stride, residual};
         return launch_gemm(e->stream, g, ws.flags.p, ws.flags.n);
     }

@@ -300,21 +300,337 @@ __global__ __launch_bounds__(256) void gemm_reduce_kernel(const GemmArgs G, cons
     G.y[m * G.y_stride + j] = v;
 }
 
+// ---------------------------------------------------------------------------
+// Q8 / Q4 weights on bf16 MFMA (v_mfma_f32_16x16x32_bf16), FP32-exact terms.
+//
+// Every int8 / int4 code is an integer of at most 8 significant bits, so it
+// is exact in bf16.  Every f32 activation x splits exactly into three bf16
+// terms: hi = x with the low 16 bits cleared, mid = the same of x - hi, and
+// lo = x - hi - mid (at most 8 significant bits left).  Each code x term
+// product has at most 16 significant bits and is exact in the FP32
+// accumulator, so sum_k x_k * c_k is formed from exact products with FP32
+// additions -- the precision class of an FP32 dot product, at three bf16
+// MFMA passes instead of the 16 FP32 ones per 16x16x64 block.
+//
+// Per 64-input scale block, a fresh FP32 block sum is scaled into the
+// running sum: acc = fma(block, scale, acc) (the per-block form of
+// linearQ8Into's dequantised dot, M:3942-4000).
+//
+// Tiling: 4 waves, each owning TM x 4 tiles of 16x16 (TM*16 activation rows
+// x 64 features); a workgroup covers TM*16 rows x 256 features.
+//  - Weights go from HBM straight into MFMA operand registers: lane
+//    (i = lane%16, q = lane/16) of feature tile tn loads the 16 codes
+//    [16q, 16q+16) of its row's block (Q8: 16 bytes, Q4: 8 bytes); the
+//    first 8 feed MFMA half 0, the rest half 1.  D blocks of weights and
+//    activations are in flight.
+//  - Activations are staged once per block into LDS as the three bf16
+//    planes, row stride 72 bf16 (conflict-free 16-byte reads of 16 rows).
+//    Lane (i, q) reads row i, inputs [16q + 8h, 16q + 8h + 8) for half h:
+//    the same K map as the weights.
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+constexpr int XBN = 256, XLD = 72;
+
+template <int TM>
+struct XTile {
+    static constexpr int BM = TM * 16;
+    static constexpr int FPT = BM * 64 / 256;  // staged floats per thread (16 or 8)
+    static constexpr int TPR = 64 / FPT;       // threads per row
+    static constexpr int NV = FPT / 4;
+    static constexpr int PLANE = BM * XLD;     // bf16 per plane
+};
+
+__device__ __forceinline__ uint32_t pk_hi16(float lo, float hi) {
+    return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
+}
+
+// One lane's 16 codes of a block: Q8 16 bytes, Q4 8 bytes.
+template <int FMT>
+struct XRaw {
+    typedef uint32_t type __attribute__((ext_vector_type(FMT == SRQ_Q8 ? 4 : 2)));
+};
+
+template <int FMT>
+__device__ __forceinline__ void xload_b(const uint8_t *__restrict__ W, const float *__restrict__ S, int64_t rows,
+                                        int64_t cols, int64_t groups, int64_t row, int64_t g, int q,
+                                        typename XRaw<FMT>::type &raw, float &scale) {
+    typedef typename XRaw<FMT>::type R;
+    if (row < rows) {
+        if constexpr (FMT == SRQ_Q8)
+            raw = *(const R *)(W + row * cols + g * kBlock + 16 * q);
+        else
+            raw = *(const R *)(W + row * (cols / 2) + g * (kBlock / 2) + 8 * q);
+        scale = S[row * groups + g];
+    } else {
+        raw = R{};
+        scale = 0.0f;
+    }
+}
+
+// Codes of one lane's block slice -> the two bf16x8 MFMA operands.
+template <int FMT>
+__device__ __forceinline__ void xcodes(const typename XRaw<FMT>::type raw, bf16x8 &h0, bf16x8 &h1) {
+    u32x4v p0, p1;
+    if constexpr (FMT == SRQ_Q8) {
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            const uint32_t d = raw[w];
+            const float c0 = (float)(int32_t)(int8_t)d, c1 = (float)(int32_t)(int8_t)(d >> 8);
+            const float c2 = (float)(int32_t)(int8_t)(d >> 16), c3 = (float)((int32_t)d >> 24);
+            const uint32_t a = pk_hi16(c0, c1), b = pk_hi16(c2, c3);
+            if (w < 2) {
+                p0[2 * w] = a;
+                p0[2 * w + 1] = b;
+            } else {
+                p1[2 * w - 4] = a;
+                p1[2 * w - 3] = b;
+            }
+        }
+    } else {
+#pragma unroll
+        for (int w = 0; w < 2; ++w) {
+            const uint32_t d = raw[w];
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                const float lo = (float)(((int32_t)(d << (28 - 8 * b))) >> 28);
+                const float hi = (float)(((int32_t)(d << (24 - 8 * b))) >> 28);
+                if (w == 0)
+                    p0[b] = pk_hi16(lo, hi);
+                else
+                    p1[b] = pk_hi16(lo, hi);
+            }
+        }
+    }
+    h0 = __builtin_bit_cast(bf16x8, p0);
+    h1 = __builtin_bit_cast(bf16x8, p1);
+}
+
+template <int TM>
+__device__ __forceinline__ void xload_a(const float *__restrict__ X, int32_t n, int64_t cols, int64_t m0, int64_t g,
+                                        int tid, float4 (&a)[XTile<TM>::NV]) {
+    constexpr int FPT = XTile<TM>::FPT, TPR = XTile<TM>::TPR, NV = XTile<TM>::NV;
+    const int r = tid / TPR, c = (tid % TPR) * FPT;
+    const int64_t m = m0 + r;
+    if (m < n) {
+        const float4 *p = (const float4 *)(X + m * cols + g * kBlock + c);
+#pragma unroll
+        for (int i = 0; i < NV; ++i) a[i] = p[i];
+    } else {
+#pragma unroll
+        for (int i = 0; i < NV; ++i) a[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+}
+
+// Splits the staged floats into the hi / mid / lo planes; returns max |x|.
+template <int TM>
+__device__ __forceinline__ float xstore_a(__bf16 *As, int tid, const float4 (&a)[XTile<TM>::NV]) {
+    constexpr int FPT = XTile<TM>::FPT, TPR = XTile<TM>::TPR, NV = XTile<TM>::NV, PLANE = XTile<TM>::PLANE;
+    const int r = tid / TPR, c = (tid % TPR) * FPT;
+    float amax = 0.0f;
+    uint32_t ph[FPT / 2], pm[FPT / 2], pl[FPT / 2];
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const float v[4] = {a[i].x, a[i].y, a[i].z, a[i].w};
+        float r1[4], r2[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            amax = fmaxf(amax, fabsf(v[e]));
+            r1[e] = v[e] - __uint_as_float(__float_as_uint(v[e]) & 0xFFFF0000u);
+            r2[e] = r1[e] - __uint_as_float(__float_as_uint(r1[e]) & 0xFFFF0000u);
+        }
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            ph[2 * i + e] = pk_hi16(v[2 * e], v[2 * e + 1]);
+            pm[2 * i + e] = pk_hi16(r1[2 * e], r1[2 * e + 1]);
+            pl[2 * i + e] = pk_hi16(r2[2 * e], r2[2 * e + 1]);
+        }
+    }
+    __bf16 *dst = As + r * XLD + c;
+#pragma unroll
+    for (int i = 0; i < FPT / 8; ++i) {
+        *(uint4 *)(dst + 8 * i) = make_uint4(ph[4 * i], ph[4 * i + 1], ph[4 * i + 2], ph[4 * i + 3]);
+        *(uint4 *)(dst + PLANE + 8 * i) = make_uint4(pm[4 * i], pm[4 * i + 1], pm[4 * i + 2], pm[4 * i + 3]);
+        *(uint4 *)(dst + 2 * PLANE + 8 * i) = make_uint4(pl[4 * i], pl[4 * i + 1], pl[4 * i + 2], pl[4 * i + 3]);
+    }
+    return amax;
+}
+
+// As gemm_kernel, for Q8 / Q4 weights and cols % 64 == 0; kper counts
+// 64-input blocks.
+//
+// Software pipeline, two blocks deep: while the MFMAs of block g run, the
+// wave converts block g+1's codes (loaded two blocks earlier) and splits
+// block g+1's activations into the other LDS stage; blocks g+2 and g+3 are
+// in flight.  Rows past the ends are clamped (weights: scale 0; activations:
+// row n-1, whose outputs are never stored) so the block body has no
+// per-lane branches.
+template <int FMT, int TM>
+__global__ __launch_bounds__(256, 2) void gemm_x3_kernel(const GemmArgs G, float *__restrict__ partial,
+                                                                       int32_t *__restrict__ wflags, const int kper) {
+    constexpr int BM = XTile<TM>::BM, NV = XTile<TM>::NV, PLANE = XTile<TM>::PLANE, TN = 4;
+    constexpr int FPT = XTile<TM>::FPT, TPR = XTile<TM>::TPR;
+    constexpr int64_t BB = FMT == SRQ_Q8 ? kBlock : kBlock / 2;  // weight bytes per row and block
+    typedef typename XRaw<FMT>::type R;
+    __shared__ __attribute__((aligned(16))) __bf16 As[2][3 * PLANE];
+    __shared__ int row_wide[BM];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int li = lane & 15, q = lane >> 4;
+    const int64_t n0 = (int64_t)blockIdx.x * XBN + wave * 64, m0 = (int64_t)blockIdx.y * BM;
+    const int64_t cols = G.cols, groups = cols / kBlock;
+    const int gbeg = (int)blockIdx.z * kper;
+    const int gend = min(gbeg + kper, (int)groups), glast = gend - 1;
+    if (tid < BM) row_wide[tid] = 0;
+
+    const uint8_t *wp[TN];
+    const float *sp[TN];
+    bool wv[TN];
+#pragma unroll
+    for (int tn = 0; tn < TN; ++tn) {
+        const int64_t row = n0 + tn * 16 + li;
+        wv[tn] = row < G.rows;
+        const int64_t rc = wv[tn] ? row : G.rows - 1;
+        wp[tn] = (const uint8_t *)G.values + rc * (BB * groups) + (BB / 4) * q;
+        sp[tn] = G.scales + rc * groups;
+    }
+    const int64_t am = min(m0 + tid / TPR, (int64_t)G.n - 1);
+    const float *ap = G.x + am * cols + (tid % TPR) * FPT;
+
+    floatx4 acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+    R raw[2][TN];
+    float sc[2][TN], s[2][TN];
+    float4 areg[2][NV];
+    bf16x8 b[2][TN][2];
+#define SRQ_LOAD_B(g, slot)                                                         \
+    _Pragma("unroll") for (int tn = 0; tn < TN; ++tn) {                              \
+        raw[slot][tn] = *(const R *)(wp[tn] + (int64_t)(g) * BB);                    \
+        const float sv = sp[tn][(g)];                                                \
+        sc[slot][tn] = wv[tn] ? sv : 0.0f;                                           \
+    }
+#define SRQ_LOAD_A(g, slot) \
+    _Pragma("unroll") for (int i = 0; i < NV; ++i) areg[slot][i] = *(const float4 *)(ap + (int64_t)(g) * kBlock + 4 * i);
+#define SRQ_CONVERT(slot)                                                           \
+    _Pragma("unroll") for (int tn = 0; tn < TN; ++tn) {                              \
+        xcodes<FMT>(raw[slot][tn], b[slot][tn][0], b[slot][tn][1]);                  \
+        s[slot][tn] = sc[slot][tn];                                                  \
+    }
+
+    SRQ_LOAD_B(gbeg, 0);
+    SRQ_LOAD_A(gbeg, 0);
+    SRQ_LOAD_B(min(gbeg + 1, glast), 1);
+    SRQ_LOAD_A(min(gbeg + 1, glast), 1);
+    SRQ_CONVERT(0);
+    SRQ_LOAD_B(min(gbeg + 2, glast), 0);
+    float amax = xstore_a<TM>(As[0], tid, areg[0]);
+    SRQ_LOAD_A(min(gbeg + 2, glast), 0);
+    __syncthreads();
+
+    for (int g0 = gbeg; g0 < gend; g0 += 2) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int g = g0 + u;
+            if (g >= gend) break;
+            const int v = u ^ 1;
+            // block g+1: codes -> operands, then refill with block g+3
+            SRQ_CONVERT(v);
+            SRQ_LOAD_B(min(g + 3, glast), v);
+            const __bf16 *as = As[u];
+#pragma unroll
+            for (int tm = 0; tm < TM; ++tm) {
+                bf16x8 a[3][2];
+#pragma unroll
+                for (int t = 0; t < 3; ++t)
+#pragma unroll
+                    for (int h = 0; h < 2; ++h)
+                        a[t][h] = *(const bf16x8 *)(as + t * PLANE + (tm * 16 + li) * XLD + 16 * q + 8 * h);
+#pragma unroll
+                for (int tn = 0; tn < TN; ++tn) {
+                    floatx4 blk = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int t = 2; t >= 0; --t)
+#pragma unroll
+                        for (int h = 0; h < 2; ++h)
+                            blk = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[t][h], b[u][tn][h], blk, 0, 0, 0);
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) acc[tm][tn][r] = __builtin_fmaf(blk[r], s[u][tn], acc[tm][tn][r]);
+                }
+            }
+            // block g+1's activations -> the other stage, then refill with block g+3
+            amax = fmaxf(amax, xstore_a<TM>(As[v], tid, areg[v]));
+            SRQ_LOAD_A(min(g + 3, glast), v);
+            __syncthreads();
+        }
+    }
+#undef SRQ_LOAD_B
+#undef SRQ_LOAD_A
+#undef SRQ_CONVERT
+    if (amax > kWideLimit) row_wide[tid / XTile<TM>::TPR] = 1;
+    __syncthreads();
+
+    // D layout of 16x16x32: lane holds rows 4*(lane/16)+r, column lane%16.
+    if (partial) {
+        float *P = partial + (int64_t)blockIdx.z * G.n * G.rows;
+        if (blockIdx.x == 0 && tid < BM && m0 + tid < G.n) wflags[(int64_t)blockIdx.z * G.n + m0 + tid] = row_wide[tid];
+#pragma unroll
+        for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int64_t m = m0 + tm * 16 + 4 * q + r;
+                if (m >= G.n) continue;
+#pragma unroll
+                for (int tn = 0; tn < TN; ++tn) {
+                    const int64_t j = n0 + tn * 16 + li;
+                    if (j < G.rows) P[m * G.rows + j] = acc[tm][tn][r];
+                }
+            }
+        return;
+    }
+#pragma unroll
+    for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int mi = tm * 16 + 4 * q + r;
+            const int64_t m = m0 + mi;
+            if (m >= G.n || row_wide[mi]) continue;
+#pragma unroll
+            for (int tn = 0; tn < TN; ++tn) {
+                const int64_t j = n0 + tn * 16 + li;
+                if (j >= G.rows) continue;
+                float v = acc[tm][tn][r];
+                if (G.residual) v = G.residual[m * G.y_stride + j] + v;
+                G.y[m * G.y_stride + j] = v;
+            }
+        }
+    for (int mi = 0; mi < BM; ++mi) {
+        if (!row_wide[mi] || m0 + mi >= G.n) continue;
+        const int64_t j = (int64_t)blockIdx.x * XBN + tid;
+        if (j < G.rows) G.y[(m0 + mi) * G.y_stride + j] = wide_output(G, m0 + mi, j);
+    }
+}
+
 struct GemmPlan {
+    bool x3;  // bf16 MFMA kernel (Q8 / Q4, cols % 64 == 0)
     int bm, slices, kper;
 };
 
 // Tile height from n; K slices so that tiles x slices reach kFillWGs
-// workgroups, each slice at least kMinSliceSteps K steps.
-GemmPlan plan_gemm(int32_t n, int64_t rows, int64_t cols) {
+// workgroups, each slice at least 256 inputs.
+GemmPlan plan_gemm(int fmt, int32_t n, int64_t rows, int64_t cols) {
     GemmPlan p;
+    p.x3 = (fmt == SRQ_Q8 || fmt == SRQ_Q4) && cols % kBlock == 0;
     p.bm = n <= 32 ? 32 : 64;
-    const int64_t tiles = ((rows + BN - 1) / BN) * ((n + p.bm - 1) / p.bm);
-    const int ksteps = (int)(cols / BK);
+    const int bn = p.x3 ? XBN : BN, bk = p.x3 ? kBlock : BK;
+    const int64_t tiles = ((rows + bn - 1) / bn) * ((n + p.bm - 1) / p.bm);
+    const int ksteps = (int)(cols / bk), min_steps = 256 / bk;
+    const int fill = kFillWGs;
     int slices = 1;
-    if (tiles < kFillWGs) {
-        const int64_t want = (kFillWGs + tiles - 1) / tiles;
-        slices = (int)std::max<int64_t>(1, std::min<int64_t>(want, ksteps / kMinSliceSteps));
+    if (tiles < fill) {
+        const int64_t want = (fill + tiles - 1) / tiles;
+        slices = (int)std::max<int64_t>(1, std::min<int64_t>(want, ksteps / min_steps));
     }
     p.kper = (ksteps + slices - 1) / slices;
     p.slices = (ksteps + p.kper - 1) / p.kper;
@@ -323,8 +639,18 @@ GemmPlan plan_gemm(int32_t n, int64_t rows, int64_t cols) {
 
 template <int FMT, int BMT>
 void launch_tiles(hipStream_t s, const GemmArgs &a, const GemmPlan &p, float *partial, int32_t *wflags) {
-    dim3 grid((unsigned)((a.rows + BN - 1) / BN), (unsigned)((a.n + BMT - 1) / BMT), (unsigned)p.slices);
-    gemm_kernel<FMT, BMT><<<grid, 256, 0, s>>>(a, partial, wflags, p.kper);
+    if constexpr (FMT == SRQ_F32) {
+        dim3 grid((unsigned)((a.rows + BN - 1) / BN), (unsigned)((a.n + BMT - 1) / BMT), (unsigned)p.slices);
+        gemm_kernel<FMT, BMT><<<grid, 256, 0, s>>>(a, partial, wflags, p.kper);
+    } else {
+        if (p.x3) {
+            dim3 grid((unsigned)((a.rows + XBN - 1) / XBN), (unsigned)((a.n + BMT - 1) / BMT), (unsigned)p.slices);
+            gemm_x3_kernel<FMT, BMT / 16><<<grid, 256, 0, s>>>(a, partial, wflags, p.kper);
+        } else {
+            dim3 grid((unsigned)((a.rows + BN - 1) / BN), (unsigned)((a.n + BMT - 1) / BMT), (unsigned)p.slices);
+            gemm_kernel<FMT, BMT><<<grid, 256, 0, s>>>(a, partial, wflags, p.kper);
+        }
+    }
 }
 
 template <int BMT>
@@ -343,9 +669,9 @@ bool gemm_ok(int fmt, int64_t cols) {
     return cols % BK == 0 && cols >= BK;
 }
 
-size_t gemm_scratch_bytes(int32_t n, int64_t rows, int64_t cols) {
-    if (n <= 0 || rows <= 0 || !gemm_ok(SRQ_F32, cols)) return 0;
-    const GemmPlan p = plan_gemm(n, rows, cols);
+size_t gemm_scratch_bytes(int fmt, int32_t n, int64_t rows, int64_t cols) {
+    if (n <= 0 || rows <= 0 || !gemm_ok(fmt, cols)) return 0;
+    const GemmPlan p = plan_gemm(fmt, n, rows, cols);
     if (p.slices == 1) return 0;
     return (size_t)p.slices * (size_t)n * ((size_t)rows + 1) * 4;
 }
@@ -353,11 +679,11 @@ size_t gemm_scratch_bytes(int32_t n, int64_t rows, int64_t cols) {
 int launch_gemm(hipStream_t s, const GemmArgs &a, void *scratch, size_t scratch_bytes) {
     if (a.n <= 0 || a.rows <= 0) return SRQ_OK;
     if (!gemm_ok(a.fmt, a.cols)) return fail(SRQ_EINVAL, "gemm: cols=%lld not a multiple of %d", (long long)a.cols, BK);
-    const GemmPlan p = plan_gemm(a.n, a.rows, a.cols);
+    const GemmPlan p = plan_gemm(a.fmt, a.n, a.rows, a.cols);
     float *partial = nullptr;
     int32_t *wflags = nullptr;
     if (p.slices > 1) {
-        const size_t need = gemm_scratch_bytes(a.n, a.rows, a.cols);
+        const size_t need = gemm_scratch_bytes(a.fmt, a.n, a.rows, a.cols);
         if (!scratch || scratch_bytes < need)
             return fail(SRQ_EINVAL, "gemm: scratch of %zu bytes, %zu needed", scratch_bytes, need);
         partial = (float *)scratch;

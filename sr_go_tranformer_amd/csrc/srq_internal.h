@@ -117,10 +117,10 @@ struct GemmArgs {
     const float *residual;  // y = residual + acc when non-null (may alias y)
 };
 // y = x . W^T (+ residual) on MFMA.  Rows holding a wide |x| are computed
-// in FP64.  scratch: gemm_scratch_bytes(n, rows, cols) bytes of device
+// in FP64.  scratch: gemm_scratch_bytes(fmt, n, rows, cols) bytes of device
 // memory for split-K partial sums (0: none needed).
 int launch_gemm(hipStream_t s, const GemmArgs &a, void *scratch, size_t scratch_bytes);
-size_t gemm_scratch_bytes(int32_t n, int64_t rows, int64_t cols);
+size_t gemm_scratch_bytes(int fmt, int32_t n, int64_t rows, int64_t cols);
 bool gemm_ok(int fmt, int64_t cols);
 
 // ------------------------------------------------------------------ glue
