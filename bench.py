@@ -443,6 +443,56 @@ def bench_continuous_batching(srq, args):
     return 0
 
 
+def bench_longctx_decode(srq, args):
+    """Mistral-7B shape, Q8: a long random prompt (default 8192 tokens)
+    prefilled in 256-token chunks, then greedy decode at that context.  The
+    paged KV cache then holds 2*ctx*kv_dim*4 bytes per layer, which every
+    decode token reads: at 8k context, 2.1 GB next to 7.6 GB of weights."""
+    from sr_go_tranformer_amd import synthetic
+    ex = srq.Executor(0)
+    prompt_n, chunk, gen = args.context_tokens, 256, args.gen_tokens
+    cfg = synthetic.shape_config("mistral-7b", prompt_n + gen)
+    model = synthetic.build(ex, cfg, "q8", args.seed)
+    hip = HipEvents()
+    stream = C.c_void_p(ex.stream)
+    pool = model.pool((prompt_n + gen) // 32 + 2)
+    cache = pool.cache((prompt_n + gen + 31) // 32)
+    prompt = synthetic.random_prompt(prompt_n, cfg.vocab, args.seed)
+    ex.synchronize()
+    a, b = hip.create(), hip.create()
+    hip.record(a, stream)
+    for lo in range(0, prompt_n, chunk):
+        model.step([cache], [prompt[lo:lo + chunk]])
+    hip.record(b, stream)
+    prefill_ms = hip.elapsed_ms(a, b)
+    first = int(model.argmax_last()[0])
+    dec = srq.Decoder(model, cache, first, gen - 1, eager=args.eager)
+    ex.synchronize()
+    hip.record(a, stream)
+    dec.run(gen - 1)
+    hip.record(b, stream)
+    dec_ms = hip.elapsed_ms(a, b)
+    dec.close()
+    kd = cfg.dim // cfg.heads * cfg.kv_heads
+    wbytes = synthetic.decode_weight_bytes(cfg, "q8")
+    mid = prompt_n + gen // 2
+    kv_bytes = 2 * mid * kd * 4 * cfg.layers
+    tok_s = (gen - 1) / (dec_ms / 1e3)
+    print(json.dumps({
+        "metric": "Mistral-7B-shape Q8 long-context greedy decode tokens/s (paged KV)",
+        "value": round(tok_s, 1), "unit": "tokens/s", "n_gpus": 1, "higher_is_better": True,
+        "dtype": "f32", "data": "synthetic",
+        "config": {"workload": "Mistral-7B shape, Q8, %d random prompt tokens in 256-token chunks, then %d greedy "
+                               "tokens" % (prompt_n, gen), "seed": args.seed,
+                   "decode_launch": "eager" if args.eager else "hip-graph"},
+        "prefill_tokens_per_s": round(prompt_n / (prefill_ms / 1e3), 1),
+        "decode_ms_per_token": round(dec_ms / (gen - 1), 4),
+        "weight_bytes_per_token": wbytes, "kv_bytes_per_token_mid": kv_bytes,
+        "achieved_gb_per_s": round((wbytes + kv_bytes) * tok_s / 1e9, 1),
+        "frac_of_hbm_peak": round((wbytes + kv_bytes) * tok_s / 8e12, 4)}), flush=True)
+    return 0
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -454,10 +504,13 @@ def main():
     ap.add_argument("--gemv-launches", type=int, default=320)
     ap.add_argument("--config", default="mistral7b-q8-decode",
                     choices=["mistral7b-q8-decode", "smollm2-q8-decode", "llama1b-q8-gemv-sweep",
-                             "mistral7b-q4mixed-prefill", "llama3b-q8-continuous-batching"],
+                             "mistral7b-q4mixed-prefill", "llama3b-q8-continuous-batching",
+                             "mistral7b-q8-longctx-decode"],
                     help="workload; the default is the headline Mistral-7B Q8 decode")
     ap.add_argument("--prompt-tokens", type=int, default=2048, help="mistral7b-q4mixed-prefill: prompt length")
-    ap.add_argument("--gen-tokens", type=int, default=128, help="mistral7b-q4mixed-prefill: generated tokens")
+    ap.add_argument("--gen-tokens", type=int, default=128,
+                    help="mistral7b-q4mixed-prefill / mistral7b-q8-longctx-decode: generated tokens")
+    ap.add_argument("--context-tokens", type=int, default=8192, help="mistral7b-q8-longctx-decode: prompt length")
     ap.add_argument("--gen-tokens-cb", type=int, default=128,
                     help="llama3b-q8-continuous-batching: output tokens per request")
     ap.add_argument("--gemv-only", action="store_true",
@@ -488,6 +541,8 @@ def main():
         return bench_q4mixed_prefill(srq, args)
     if args.config == "llama3b-q8-continuous-batching":
         return bench_continuous_batching(srq, args)
+    if args.config == "mistral7b-q8-longctx-decode":
+        return bench_longctx_decode(srq, args)
 
     t_start = time.perf_counter()
     ex = srq.Executor(0)

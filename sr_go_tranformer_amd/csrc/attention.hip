@@ -30,6 +30,7 @@ constexpr int kMaxHd = 256;
 // ones (prefill) the split and combine kernels, whose many workgroups would
 // otherwise each pay the merge's cache write-back and invalidation.
 constexpr int kFusedRows = 4;
+constexpr int kFusedSplits = 16;  // splits of 64 positions: context <= 1024
 
 __device__ __forceinline__ const float *kv_row(const RowMeta &m, int sess, int pos, int kvdim, int which) {
     const int page = m.pages[(int64_t)sess * m.pt_stride + pos / kPageTokens];
@@ -266,6 +267,72 @@ __global__ __launch_bounds__(256) void attn_split_fast_kernel(const AttnArgs A, 
     }
 }
 
+constexpr int kMergeChunk = 256;  // splits per pass of the weight table
+constexpr int kMergePairs = kMaxGroup * kMaxHd / 256;
+constexpr int kMergeBatch = 16;   // partial loads in flight per (head, dim) pair
+
+// Merge of split partials (m_i, l_i, o_i) for heads h0 .. h0+nh-1 of a row,
+// by all 256 threads of the workgroup:
+//   M = max_i m_i, l = sum_i l_i exp(m_i - M) (FP64), lse = M + log(l),
+//   out_j = sum_i f32(exp(m_i - lse)) * o_i[j], FMA in split order.
+// One wave per head forms M and l (lanes stride the splits, then a
+// butterfly); the (head, dim) pairs spread over the threads, each pair
+// loading kMergeBatch splits at a time.
+__device__ __forceinline__ void merge_splits(const AttnArgs &A, const float *part, int nsplit, int row, int h0,
+                                             int nh, int hd, int used, float (*cf)[kMergeChunk], double *lse) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    for (int g = wave; g < nh; g += 4) {
+        const int h = h0 + g;
+        float M = -FLT_MAX;
+        for (int i = lane; i < used; i += 64) M = fmaxf(M, partial((float *)part, row, h, i, A.heads, nsplit, hd)[0]);
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
+        double l = 0.0;
+        for (int i = lane; i < used; i += 64) {
+            const float *p = partial((float *)part, row, h, i, A.heads, nsplit, hd);
+            l += *(const double *)(p + 2) * exp((double)p[0] - (double)M);
+        }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) l += __shfl_xor(l, o, 64);
+        if (lane == 0) lse[g] = (double)M + log(l);
+    }
+    __syncthreads();
+    float o[kMergePairs];
+#pragma unroll
+    for (int k = 0; k < kMergePairs; ++k) o[k] = 0.0f;
+    for (int c0 = 0; c0 < used; c0 += kMergeChunk) {
+        const int cnt = min(kMergeChunk, used - c0);
+        for (int t = tid; t < nh * cnt; t += 256) {
+            const int g = t / cnt, i = t - g * cnt;
+            cf[g][i] = (float)exp((double)partial((float *)part, row, h0 + g, c0 + i, A.heads, nsplit, hd)[0] - lse[g]);
+        }
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < kMergePairs; ++k) {
+            const int pidx = tid + 256 * k;
+            if (pidx >= nh * hd) break;
+            const int g = pidx / hd, j = pidx - g * hd;
+            const float *pb = partial((float *)part, row, h0 + g, c0, A.heads, nsplit, hd) + 4 + j;
+            for (int i0 = 0; i0 < cnt; i0 += kMergeBatch) {
+                float v[kMergeBatch];
+#pragma unroll
+                for (int b = 0; b < kMergeBatch; ++b) v[b] = pb[(int64_t)min(i0 + b, cnt - 1) * (hd + 4)];
+#pragma unroll
+                for (int b = 0; b < kMergeBatch; ++b)
+                    if (i0 + b < cnt) o[k] = __builtin_fmaf(cf[g][i0 + b], v[b], o[k]);
+            }
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int k = 0; k < kMergePairs; ++k) {
+        const int pidx = tid + 256 * k;
+        if (pidx >= nh * hd) break;
+        const int g = pidx / hd, j = pidx - g * hd;
+        A.out[(int64_t)row * A.heads * hd + (int64_t)(h0 + g) * hd + j] = o[k];
+    }
+}
+
 // Fused split + combine for decode-sized batches, head_dim 64 / 128.
 // Workgroup (row, kv head, split) loads its K and V rows together (one round
 // of memory latency), scores all query heads of the GQA group, writes its
@@ -285,7 +352,8 @@ __global__ __launch_bounds__(256) void attn_fused_kernel(const AttnArgs A, float
     __shared__ float qs[kMaxGroup * HD];
     __shared__ float sc[kMaxGroup][kSplit];
     __shared__ float4 red[KG][DG];
-    __shared__ float cf[kMaxGroup][64];
+    __shared__ float cf[kMaxGroup][kMergeChunk];
+    __shared__ double lse[kMaxGroup];
     __shared__ int last;
 
     const int row = blockIdx.x, kh = blockIdx.y, sp = blockIdx.z;
@@ -403,68 +471,18 @@ __global__ __launch_bounds__(256) void attn_fused_kernel(const AttnArgs A, float
     if (!last) return;
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     if (tid == 0) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    // lse = M + log(sum_i l_i exp(m_i - M)), factors f32(exp(m_i - lse)):
-    // one wave per head, splits in chunks of 64 lanes.
-    for (int g = wave; g < G; g += 4) {
-        const int h = kh * G + g;
-        float M = -FLT_MAX;
-        for (int i = lane; i < used; i += 64) M = fmaxf(M, partial(part, row, h, i, A.heads, nsplit, HD)[0]);
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
-        double l = 0.0;
-        for (int i = lane; i < used; i += 64) {
-            const float *p = partial(part, row, h, i, A.heads, nsplit, HD);
-            l += *(const double *)(p + 2) * exp((double)p[0] - (double)M);
-        }
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) l += __shfl_xor(l, o, 64);
-        const double lse = (double)M + log(l);
-        for (int i0 = 0; i0 < used; i0 += 64) {
-            const int i = i0 + lane;
-            if (i < used) cf[g][lane] = (float)exp((double)partial(part, row, h, i, A.heads, nsplit, HD)[0] - lse);
-            // out_j += the chunk's splits, in split order
-            for (int j = lane; j < HD; j += 64) {
-                float o = i0 == 0 ? 0.0f : A.out[(int64_t)row * A.heads * HD + (int64_t)h * HD + j];
-                const int cnt_i = min(64, used - i0);
-                for (int ii = 0; ii < cnt_i; ++ii)
-                    o = __builtin_fmaf(cf[g][ii], partial(part, row, h, i0 + ii, A.heads, nsplit, HD)[4 + j], o);
-                A.out[(int64_t)row * A.heads * HD + (int64_t)h * HD + j] = o;
-            }
-        }
-    }
+    merge_splits(A, part, nsplit, row, kh * G, G, HD, used, cf, lse);
 }
 
 // lse and the weighted sum of split partials for one (row, head).
 __global__ __launch_bounds__(256) void attn_combine_kernel(const AttnArgs A, const float *__restrict__ part,
                                                            int nsplit) {
-    __shared__ float cf[1024];
-    __shared__ double red[4];
-    const int row = blockIdx.x, h = blockIdx.y, tid = threadIdx.x, hd = A.head_dim;
+    __shared__ float cf[kMaxGroup][kMergeChunk];
+    __shared__ double lse[kMaxGroup];
+    const int row = blockIdx.x, h = blockIdx.y;
     const int len = A.meta.pos[row] + 1;
     const int used = min(nsplit, (len + kSplit - 1) / kSplit);
-    float M = -FLT_MAX;
-    for (int i = 0; i < used; ++i) M = fmaxf(M, partial((float *)part, row, h, i, A.heads, nsplit, hd)[0]);
-    double l = 0.0;
-    for (int i = tid; i < used; i += 256) {
-        const float *p = partial((float *)part, row, h, i, A.heads, nsplit, hd);
-        l += *(const double *)(p + 2) * exp((double)p[0] - (double)M);
-    }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) l += __shfl_xor(l, o, 64);
-    if ((tid & 63) == 0) red[tid >> 6] = l;
-    __syncthreads();
-    l = red[0] + red[1] + red[2] + red[3];
-    const double lse = (double)M + log(l);
-    for (int i = tid; i < used; i += 256) {
-        const float *p = partial((float *)part, row, h, i, A.heads, nsplit, hd);
-        cf[i] = (float)exp((double)p[0] - lse);
-    }
-    __syncthreads();
-    for (int j = tid; j < hd; j += 256) {
-        float o = 0.0f;
-        for (int i = 0; i < used; ++i) o = __builtin_fmaf(cf[i], partial((float *)part, row, h, i, A.heads, nsplit, hd)[4 + j], o);
-        A.out[(int64_t)row * A.heads * hd + (int64_t)h * hd + j] = o;
-    }
+    merge_splits(A, part, nsplit, row, h, 1, A.head_dim, used, cf, lse);
 }
 
 }  // namespace
@@ -484,8 +502,11 @@ int launch_attention(hipStream_t s, const AttnArgs &a, float *scratch, int32_t *
     if (nsplit > 1024) return fail(SRQ_EINVAL, "attention: %d positions exceed the split table", a.max_len);
     const dim3 grid(a.n, a.kv_heads, nsplit);
     const bool fast = a.head_dim == 128 || a.head_dim == 64;
-    if (fast && a.n <= kFusedRows) {
-        // Decode-sized batches: one launch, the last split merges.
+    if (fast && a.n <= kFusedRows && nsplit <= kFusedSplits) {
+        // Decode-sized batches at short context: one launch, the last split
+        // merges.  Each split then publishes its partials with an agent-scope
+        // release (an L2 writeback on its XCD); past kFusedSplits splits those
+        // cost more than the second launch of split + combine.
         if (a.head_dim == 128)
             attn_fused_kernel<128><<<grid, 256, 0, s>>>(a, scratch, nsplit, counters);
         else

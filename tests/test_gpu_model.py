@@ -162,6 +162,32 @@ def test_greedy_generate_and_decoder(ex):
         d.close()
 
 
+def test_long_context_decode(ex):
+    """Decode past 1024 positions at head_dim 128: more than 16 attention
+    splits, so the split + combine path replaces the fused one.  Greedy
+    tokens (graph-replayed and eager decoders, batched steps) against the
+    oracle's."""
+    cfg = srq.make_config(512, 256, 2, 2, 1, 512, 1400, 10000.0, 1e-5, True)
+    m, norms = gpu_models.synthetic(ex, cfg, "q8", 5)
+    om = gpu_models.oracle_from_device(ex, m, cfg, norms)
+    ids = [int(t) for t in np.random.default_rng(3).integers(0, cfg.vocab, size=1100)]
+    want, _ = oracle.greedy(om, ids, 12, 256)
+    pool = m.pool(3 * 36)
+    for eager in (False, True):
+        c = pool.cache(36)
+        for lo in range(0, len(ids), 256):
+            m.step([c], [ids[lo:lo + 256]])
+        first = int(m.argmax_last()[0])
+        assert first == want[0]
+        d = srq.Decoder(m, c, first, 11, eager=eager)
+        d.run(11)
+        assert d.tokens() == want[1:12], (eager, d.tokens(), want[1:12])
+        d.close()
+    c = pool.cache(36)
+    got = m.generate_greedy(c, ids, 12, chunk=256)
+    assert got == want
+
+
 def test_smollm2_shape_greedy_identity(ex):
     """SmolLM2-135M architecture (576 / 30 layers / 9:3 heads / 1536 /
     49152 tied), seeded N(0, 0.02) weights, Q8; 32-token prompt (one MFMA

@@ -226,6 +226,33 @@ def test_linear_gemm_wide_rows(ex, shape):
     near(got, oracle.linear_closed_f64(ow, x), 2e-5)
 
 
+@pytest.mark.parametrize("fmt", [srq.Q8, srq.Q4])
+@pytest.mark.parametrize("n", [20, 64, 256])
+@pytest.mark.parametrize("biased", [False, True])
+def test_gemm_error_is_fp32_class(ex, fmt, n, biased):
+    """The Q8/Q4 GEMM runs on bf16 MFMA with every activation split into
+    three bf16 terms, which is exact; its error against the FP64 dot product
+    of the same codes stays at FP32-accumulation level (2e-6 of sum |x||w|).
+    biased: activations with their 8 low mantissa bits set and weights >= 0,
+    so a dropped lowest term would err the same way on every product
+    (~3e-5 of sum |x||w|) instead of averaging out."""
+    print("gemm fp32 class", fmt, n, biased, flush=True)
+    rows, cols = 384, 4096
+    rng = np.random.default_rng(n + 7 * biased)
+    dense = rng.normal(0, 0.02, size=(rows, cols)).astype(np.float32)
+    x = rng.normal(0, 1.0, size=(n, cols)).astype(np.float32)
+    if biased:
+        dense = np.abs(dense)
+        x = rng.uniform(1.0, 2.0, size=(n, cols)).astype(np.float32)
+        x = (x.view(np.uint32) | np.uint32(0xFF)).view(np.float32)
+    w, ow = _weights(ex, dense, fmt)
+    got = srq.linear(ex, w, x).astype(np.float64)
+    exact = oracle.linear_closed_f64(ow, x)
+    mag = np.abs(x).astype(np.float64) @ np.abs(ow.dequant()).astype(np.float64).T
+    err = (np.abs(got - exact) / mag).max()
+    assert err < 2e-6, err
+
+
 def test_linear_mistral_mlp_full_shape(ex):
     """The 7B decode shape 14336 x 4096, batch 1, against the oracle."""
     rng = oracle.RNG(2024)
