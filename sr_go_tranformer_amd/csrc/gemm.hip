@@ -33,7 +33,8 @@ namespace srq {
 namespace {
 
 constexpr int BN = 128, BK = 32, LDK = BK + 4;
-constexpr int kFillWGs = 512;      // two resident workgroups on each of 256 CUs
+constexpr int kCUs = 256;          // MI355X compute units
+constexpr int kFillWGs = 512;      // two resident workgroups on each CU
 constexpr int kMinSliceSteps = 8;  // K steps per split-K slice (256 inputs)
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
@@ -617,8 +618,9 @@ struct GemmPlan {
     int bm, slices, kper;
 };
 
-// Tile height from n; K slices so that tiles x slices reach kFillWGs
-// workgroups, each slice at least 256 inputs.
+// Tile height from n.  With fewer tiles than CUs, K slices bring the grid
+// to kFillWGs workgroups, each slice at least 256 inputs; from one tile per
+// CU up, the slices' partial sums would cost more than the idle CUs.
 GemmPlan plan_gemm(int fmt, int32_t n, int64_t rows, int64_t cols) {
     GemmPlan p;
     p.x3 = (fmt == SRQ_Q8 || fmt == SRQ_Q4) && cols % kBlock == 0;
@@ -626,10 +628,9 @@ GemmPlan plan_gemm(int fmt, int32_t n, int64_t rows, int64_t cols) {
     const int bn = p.x3 ? XBN : BN, bk = p.x3 ? kBlock : BK;
     const int64_t tiles = ((rows + bn - 1) / bn) * ((n + p.bm - 1) / p.bm);
     const int ksteps = (int)(cols / bk), min_steps = 256 / bk;
-    const int fill = kFillWGs;
     int slices = 1;
-    if (tiles < fill) {
-        const int64_t want = (fill + tiles - 1) / tiles;
+    if (tiles < kCUs) {
+        const int64_t want = (kFillWGs + tiles - 1) / tiles;
         slices = (int)std::max<int64_t>(1, std::min<int64_t>(want, ksteps / min_steps));
     }
     p.kper = (ksteps + slices - 1) / slices;
