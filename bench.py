@@ -413,14 +413,14 @@ def bench_continuous_batching(srq, args):
         steps += 1
         sel = [k for k in range(len(active)) if want[k]]
         if sel:
-            # the step's logits are [sessions x vocab] with unselected rows
-            # zeroed; sample every row and keep the selected ones
-            st = rng[active].copy()
-            ids = srq.sample(ex, dev, len(active), cfg.vocab, params, st)
-            for k in sel:
+            # the step's logits are [sessions x vocab]; sample the rows of the
+            # sessions that asked for a token
+            st = rng[[active[k] for k in sel]].copy()
+            ids = srq.sample(ex, dev, len(sel), cfg.vocab, params, st, row_ids=sel)
+            for j, k in enumerate(sel):
                 i = active[k]
-                rng[i] = st[k]
-                outputs[i].append(int(ids[k]))
+                rng[i] = st[j]
+                outputs[i].append(int(ids[j]))
         for k, i in enumerate(active):
             if not decoding[k]:
                 cursor[i] += len(chunks[k])

@@ -201,14 +201,16 @@ int srq_step(srq_exec *e, srq_model *m, int32_t sessions, srq_cache *const *cach
  * logit of a row is not finite. */
 int srq_argmax(srq_exec *e, const float *logits, int32_t rows, int32_t vocab, int32_t *ids);
 
-/* sampleWithBlocked (M:7320-7426) for rows of device logits [rows x vocab].
+/* sampleWithBlocked (M:7320-7426) for rows of device logits [* x vocab].
  * Per row: value = f64(logit), repeat penalty for ids in the row's history
  * (divide if > 0, else multiply), the blocked id excluded; temperature 0 is
  * the first maximum (lowest id on ties) with no draw; otherwise candidates
  * ordered by value descending then id ascending, cut to top_k (0: off), then
  * to the shortest prefix holding top_p of the mass (>= 1: off), and one
  * SplitMix64 Float64 draw picks the candidate (M:7360-7425).  Host arrays:
- * history [rows x history_stride] with history_len[rows] valid ids (both
+ * row_ids [rows] (nullable: row k is logits row k) names the logits row each
+ * of the rows samples, so a caller samples only the sessions of a step that
+ * want a token; history [rows x history_stride] with history_len[rows] valid ids (both
  * nullable), blocked [rows] (-1 none; nullable), rng_state [rows] (in/out:
  * advanced by one draw per row sampled at temperature != 0), ids [rows] out.
  * SRQ_ENONFINITE if a row holds a non-finite logit; SRQ_EINVAL if a row has
@@ -221,7 +223,8 @@ typedef struct {
     double top_p;
     double repeat_penalty;
 } srq_sampling;
-int srq_sample(srq_exec *e, const float *logits, int32_t rows, int32_t vocab, const srq_sampling *params,
+int srq_sample(srq_exec *e, const float *logits, int32_t rows, const int32_t *row_ids, int32_t vocab,
+               const srq_sampling *params,
                const int32_t *history, const int32_t *history_len, int32_t history_stride, const int32_t *blocked,
                uint64_t *rng_state, int32_t *ids);
 

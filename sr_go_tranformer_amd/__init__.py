@@ -108,7 +108,7 @@ def _declare(L):
         "srq_cache_read": (C.c_int, [P, P, I32, I32, I32, P, P]),
         "srq_step": (C.c_int, [P, P, I32, P, P, P, P, PP, P, P]),
         "srq_argmax": (C.c_int, [P, P, I32, I32, P]),
-        "srq_sample": (C.c_int, [P, P, I32, I32, P, P, P, I32, P, P, P]),
+        "srq_sample": (C.c_int, [P, P, I32, P, I32, P, P, P, I32, P, P, P]),
         "srq_decoder_create": (C.c_int, [P, P, P, I32, I32, I32, PP]),
         "srq_decoder_run": (C.c_int, [P, I32]),
         "srq_decoder_tokens": (C.c_int, [P, P, C.POINTER(I32)]),
@@ -455,9 +455,10 @@ class Sampling(C.Structure):
                 ("repeat_penalty", C.c_double)]
 
 
-def sample(ex, logits_ptr, rows, vocab, params, rng_states, histories=None, blocked=None):
+def sample(ex, logits_ptr, rows, vocab, params, rng_states, histories=None, blocked=None, row_ids=None):
     """srq_sample over device logits; rng_states (np.uint64 [rows]) is
-    advanced in place; histories: list of per-row id lists or None."""
+    advanced in place; histories: list of per-row id lists or None; row_ids:
+    the logits row each of the rows samples (None: row k)."""
     rng = np.ascontiguousarray(rng_states, np.uint64)
     assert rng.shape == (rows,) and rng is rng_states, "rng_states must be a contiguous uint64 array"
     ids = np.zeros(rows, np.int32)
@@ -471,9 +472,10 @@ def sample(ex, logits_ptr, rows, vocab, params, rng_states, histories=None, bloc
             hist[r, :len(h)] = h
             hl[r] = len(h)
     blk = None if blocked is None else np.ascontiguousarray(blocked, np.int32)
+    sel = None if row_ids is None else np.ascontiguousarray(row_ids, np.int32)
     ptr = lambda a: None if a is None else _np_ptr(a)
-    check(lib().srq_sample(ex.h, logits_ptr, rows, vocab, C.byref(params), ptr(hist), ptr(hl), stride, ptr(blk),
-                           _np_ptr(rng), _np_ptr(ids)))
+    check(lib().srq_sample(ex.h, logits_ptr, rows, ptr(sel), vocab, C.byref(params), ptr(hist), ptr(hl), stride,
+                           ptr(blk), _np_ptr(rng), _np_ptr(ids)))
     return ids
 
 

@@ -1120,9 +1120,9 @@ extern "C" int srq_argmax(srq_exec *e, const float *logits, int32_t rows, int32_
     return check_err_flag(e, SRQ_ENONFINITE, "non-finite HF logits");
 }
 
-extern "C" int srq_sample(srq_exec *e, const float *logits, int32_t rows, int32_t vocab, const srq_sampling *params,
-                          const int32_t *history, const int32_t *history_len, int32_t history_stride,
-                          const int32_t *blocked, uint64_t *rng_state, int32_t *ids) {
+extern "C" int srq_sample(srq_exec *e, const float *logits, int32_t rows, const int32_t *row_ids, int32_t vocab,
+                          const srq_sampling *params, const int32_t *history, const int32_t *history_len,
+                          int32_t history_stride, const int32_t *blocked, uint64_t *rng_state, int32_t *ids) {
     if (!e || !logits || !params || !rng_state || !ids) return fail(SRQ_EINVAL, "null pointer");
     if (rows < 1 || vocab < 1) return fail(SRQ_EINVAL, "empty logits");
     if (!(params->temperature >= 0) || !(params->repeat_penalty > 0) || params->top_k < 0 || !(params->top_p > 0))
@@ -1130,18 +1130,22 @@ extern "C" int srq_sample(srq_exec *e, const float *logits, int32_t rows, int32_
     if (history && (!history_len || history_stride < 0)) return fail(SRQ_EINVAL, "history without lengths");
     for (int32_t r = 0; history && r < rows; ++r)
         if (history_len[r] < 0 || history_len[r] > history_stride) return fail(SRQ_EINVAL, "bad history length");
+    for (int32_t r = 0; row_ids && r < rows; ++r)
+        if (row_ids[r] < 0) return fail(SRQ_EINVAL, "negative logits row");
     DeviceGuard g(e->device);
     Workspace &ws = e->ws;
     const size_t hist_words = history ? (size_t)rows * history_stride : 0;
-    // [rng: 2*rows][ids: rows][blocked: rows][history_len: rows][history]
-    const size_t words = (size_t)rows * 5 + hist_words;
+    // [rng: 2*rows][ids: rows][blocked: rows][history_len: rows][row_ids: rows][history]
+    const size_t words = (size_t)rows * 6 + hist_words;
     SRQ_CHECK(ensure(ws.SMP, words * 4, e->stream));
     SRQ_CHECK(ensure(ws.SMPP, sample_scratch_bytes(rows, vocab), e->stream));
     int32_t *d = as<int32_t>(ws.SMP);
     uint64_t *d_rng = (uint64_t *)d;
-    int32_t *d_ids = d + 2 * rows, *d_blk = d + 3 * rows, *d_hl = d + 4 * rows, *d_hist = d + 5 * rows;
+    int32_t *d_ids = d + 2 * rows, *d_blk = d + 3 * rows, *d_hl = d + 4 * rows, *d_rows = d + 5 * rows;
+    int32_t *d_hist = d + 6 * rows;
     SRQ_HIP(hipMemcpyAsync(d_rng, rng_state, (size_t)rows * 8, hipMemcpyHostToDevice, e->stream));
     if (blocked) SRQ_HIP(hipMemcpyAsync(d_blk, blocked, (size_t)rows * 4, hipMemcpyHostToDevice, e->stream));
+    if (row_ids) SRQ_HIP(hipMemcpyAsync(d_rows, row_ids, (size_t)rows * 4, hipMemcpyHostToDevice, e->stream));
     if (history) {
         SRQ_HIP(hipMemcpyAsync(d_hl, history_len, (size_t)rows * 4, hipMemcpyHostToDevice, e->stream));
         if (hist_words)
@@ -1149,6 +1153,7 @@ extern "C" int srq_sample(srq_exec *e, const float *logits, int32_t rows, int32_
     }
     SampleArgs a{};
     a.logits = logits;
+    a.row_ids = row_ids ? d_rows : nullptr;
     a.rows = rows;
     a.vocab = vocab;
     a.temperature = params->temperature;
@@ -1178,7 +1183,7 @@ extern "C" int srq_sample(srq_exec *e, const float *logits, int32_t rows, int32_
     return SRQ_OK;
 }
 
-// ----------------------------------------------------------- greedy decoder// ----------------------------------------------------------- greedy decoder
+// ----------------------------------------------------------- greedy decoder
 struct srq_decoder {
     srq_exec *e = nullptr;
     srq_model *m = nullptr;

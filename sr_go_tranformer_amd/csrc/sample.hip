@@ -33,6 +33,8 @@ constexpr int kBuckets = 2048;
 constexpr int kList = 2048;    // candidates of one bucket sorted in LDS
 constexpr int kLevels = 4;     // bucket refinements before giving up
 constexpr double kFix = 17592186044416.0;  // 2^44: mass of probability 1
+// The scans give each thread two buckets / two sorted candidates.
+static_assert(kBuckets == 2 * kST && kList == 2 * kST, "two entries per thread");
 
 struct Cand {  // a position in candidate order; id INT_MAX = past every candidate
     double v;
@@ -50,7 +52,6 @@ struct SampleLds {
     int li[kList];
     unsigned long long lp[kList];
     unsigned long long scan[kST];
-    int scan_i[kST];
     double red_d[kST / 64];
     int red_i[kST / 64];
     unsigned long long red_u[kST / 64];
@@ -127,12 +128,25 @@ __device__ __forceinline__ int bucket_of(double v, double lo, double scale) {
 
 enum { CUT_COUNT = 0, CUT_MASS_GE = 1, CUT_MASS_GT = 2 };
 
+// Smallest v over the workgroup (wave butterfly, then the waves' minima).
+__device__ __forceinline__ int block_min_int(int v, SampleLds &s) {
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = min(v, __shfl_xor(v, o, 64));
+    if ((tid & 63) == 0) s.red_i[tid >> 6] = v;
+    __syncthreads();
+    int r = s.red_i[0];
+    for (int w = 1; w < kST / 64; ++w) r = min(r, s.red_i[w]);
+    __syncthreads();
+    return r;
+}
+
 __global__ __launch_bounds__(kST) void sample_kernel(const SampleArgs A, unsigned long long *__restrict__ pscr) {
     extern __shared__ uint32_t seen[];  // history bitmap, (vocab + 31) / 32 words
     __shared__ SampleLds s;
     const int row = blockIdx.x, tid = threadIdx.x;
     const int vocab = A.vocab;
-    const float *lg = A.logits + (int64_t)row * vocab;
+    const float *lg = A.logits + (int64_t)(A.row_ids ? A.row_ids[row] : row) * vocab;
     unsigned long long *P = pscr + (int64_t)row * vocab;
     const int blocked = A.blocked ? A.blocked[row] : -1;
     const double T = A.temperature, rp = A.repeat_penalty;
@@ -266,11 +280,8 @@ __global__ __launch_bounds__(kST) void sample_kernel(const SampleArgs A, unsigne
                 if (hit(before_t + w0) && (w0 > 0 || mode == CUT_COUNT)) mine = 2 * tid;
                 else if (hit(before_t + w0 + w1)) mine = 2 * tid + 1;
                 if (mine != INT_MAX && s.hcount[kBuckets - 1 - mine] == 0) mine = INT_MAX;
-                s.scan_i[tid] = mine;
-                __syncthreads();
+                const int first = block_min_int(mine, s);
                 if (tid == 0) {
-                    int first = INT_MAX;
-                    for (int t = 0; t < kST; ++t) first = min(first, s.scan_i[t]);
                     s.bucket = first;
                     if (first != INT_MAX) {
                         const int owner = first / 2;
@@ -328,37 +339,48 @@ __global__ __launch_bounds__(kST) void sample_kernel(const SampleArgs A, unsigne
                     if (member(i, v) && inside(v) && bucket_of(v, lo, scale) == b) atomicAdd(&s.hcount[i / width], 1u);
                 }
                 __syncthreads();
-                if (tid == 0) {
-                    unsigned long long c = 0;
-                    int k = 0;
-                    for (; k < kBuckets; ++k) {
-                        if (c + s.hcount[k] >= m) break;
-                        c += s.hcount[k];
+                {
+                    // first id bucket whose running count reaches m: thread t
+                    // owns id buckets 2t and 2t+1 (ascending ids)
+                    const unsigned long long w0 = s.hcount[2 * tid], w1 = s.hcount[2 * tid + 1];
+                    s.scan[tid] = w0 + w1;
+                    __syncthreads();
+                    for (int o = 1; o < kST; o <<= 1) {  // inclusive scan
+                        const unsigned long long add = tid >= o ? s.scan[tid - o] : 0ull;
+                        __syncthreads();
+                        s.scan[tid] += add;
+                        __syncthreads();
                     }
-                    s.bucket = k;
-                    s.above = c;  // candidates of lower ids
-                    s.list_n = 0;
+                    const unsigned long long b0 = tid ? s.scan[tid - 1] : 0ull;
+                    const int mine = b0 + w0 >= m ? 2 * tid : b0 + w0 + w1 >= m ? 2 * tid + 1 : INT_MAX;
+                    const int first = block_min_int(mine, s);
+                    if (first != INT_MAX && mine == first) {
+                        s.bucket = first;
+                        s.above = (first & 1) ? b0 + w0 : b0;  // candidates of lower ids
+                    }
+                    if (tid == 0) s.list_n = 0;
+                    __syncthreads();
                 }
-                __syncthreads();
                 const int ib = s.bucket;
                 for (int i = ib * width + tid; i < min(vocab, (ib + 1) * width); i += kST) {
                     const double v = value(i, lg[i]);
                     if (member(i, v) && inside(v) && bucket_of(v, lo, scale) == b) s.li[atomicAdd(&s.list_n, 1)] = i;
                 }
                 __syncthreads();
-                if (tid == 0) {
-                    // the (m - above)-th smallest gathered id (at most `width` of them)
+                {
+                    // the (m - above)-th smallest gathered id (ids are distinct,
+                    // at most `width` of them): the one with that many below it
                     const int want = (int)(m - s.above) - 1, ln = s.list_n;
-                    for (int a = 0; a <= want; ++a) {
-                        int mn = a;
-                        for (int c2 = a + 1; c2 < ln; ++c2)
-                            if (s.li[c2] < s.li[mn]) mn = c2;
-                        const int t2 = s.li[a];
-                        s.li[a] = s.li[mn], s.li[mn] = t2;
+                    for (int t = tid; t < ln; t += kST) {
+                        const int id = s.li[t];
+                        int rank = 0;
+                        for (int c2 = 0; c2 < ln; ++c2) rank += s.li[c2] < id;
+                        if (rank == want) {
+                            s.cut = Cand{bmn, id};
+                            s.cum = above + (mode == CUT_COUNT ? m : m * pe);
+                            s.found = 1;
+                        }
                     }
-                    s.cut = Cand{bmn, s.li[want]};
-                    s.cum = above + (mode == CUT_COUNT ? m : m * pe);
-                    s.found = 1;
                 }
                 __syncthreads();
                 return;
@@ -410,16 +432,29 @@ __global__ __launch_bounds__(kST) void sample_kernel(const SampleArgs A, unsigne
                     __syncthreads();
                 }
             }
-            if (tid == 0) {
-                unsigned long long c = above;
-                for (int k = 0; k < ln; ++k) {
-                    c += mode == CUT_COUNT ? 1ull : s.lp[k];
-                    if (mode == CUT_MASS_GT ? c > target : c >= target) {
-                        s.cut = Cand{s.lv[k], s.li[k]};
-                        s.cum = c;
-                        s.found = 1;
-                        break;
-                    }
+            // The first sorted candidate whose running total hits: thread t
+            // owns entries 2t and 2t+1; an inclusive scan of the pairs gives
+            // every running total at once.
+            {
+                const int k0 = 2 * tid, k1 = k0 + 1;
+                const unsigned long long w0 = k0 < ln ? (mode == CUT_COUNT ? 1ull : s.lp[k0]) : 0ull;
+                const unsigned long long w1 = k1 < ln ? (mode == CUT_COUNT ? 1ull : s.lp[k1]) : 0ull;
+                s.scan[tid] = w0 + w1;
+                __syncthreads();
+                for (int o = 1; o < kST; o <<= 1) {  // inclusive scan
+                    const unsigned long long add = tid >= o ? s.scan[tid - o] : 0ull;
+                    __syncthreads();
+                    s.scan[tid] += add;
+                    __syncthreads();
+                }
+                const unsigned long long c0 = above + (tid ? s.scan[tid - 1] : 0ull) + w0, c1 = c0 + w1;
+                auto hit = [&](unsigned long long c) { return mode == CUT_MASS_GT ? c > target : c >= target; };
+                const int mine = k0 < ln && hit(c0) ? k0 : k1 < ln && hit(c1) ? k1 : INT_MAX;
+                const int first = block_min_int(mine, s);
+                if (first != INT_MAX && mine == first) {
+                    s.cut = Cand{s.lv[first], s.li[first]};
+                    s.cum = (first & 1) ? c1 : c0;
+                    s.found = 1;
                 }
             }
             __syncthreads();

@@ -139,7 +139,8 @@ int launch_row_plan(hipStream_t s, const RowMeta &meta, int32_t n, int32_t kvdim
 
 // -------------------------------------------------------------- sampling
 struct SampleArgs {
-    const float *logits;         // [rows x vocab]
+    const float *logits;         // [* x vocab]
+    const int32_t *row_ids;      // [rows]: logits row of each sampled row, or null (row k)
     int32_t rows, vocab;
     double temperature;          // 0: greedy
     int32_t top_k;               // 0: off

@@ -110,6 +110,27 @@ def test_sample_draws_follow_the_distribution(ex):
     assert np.abs(counts / counts.sum() - p).max() < 0.03
 
 
+def test_sample_row_ids_select_rows(ex):
+    """row_ids: a subset of the logits rows, in any order, samples exactly as
+    those rows would compacted (the sessions of a step that want a token)."""
+    rng = np.random.default_rng(21)
+    rows, vocab = 9, 4099
+    logits = rng.normal(0, 2.0, size=(rows, vocab)).astype(np.float32)
+    logits[3] = 0.0  # a zeroed row that is not sampled
+    buf = srq.DeviceBuffer.from_numpy(ex, logits)
+    sel = [7, 2, 5, 0]
+    seeds = rng.integers(0, 2**63, size=len(sel), dtype=np.uint64)
+    for t, k, p in [(0.9, 40, 0.95), (0.8, 0, 0.9), (0.0, 0, 1.0)]:
+        st = seeds.copy()
+        got = srq.sample(ex, buf.ptr, len(sel), vocab, srq.Sampling(t, k, p, 1.0), st, row_ids=sel)
+        want, wst = oracle_rows(logits[sel], t, k, p, 1.0, seeds)
+        assert np.array_equal(got, want), (t, got, want)
+        assert np.array_equal(st, wst)
+    with pytest.raises(srq.SrqError) as e:
+        srq.sample(ex, buf.ptr, 2, vocab, srq.Sampling(0.8, 0, 1.0, 1.0), seeds[:2].copy(), row_ids=[1, -1])
+    assert e.value.code == srq.EINVAL
+
+
 def test_sample_errors(ex):
     logits = np.zeros((2, 33), np.float32)
     logits[1, 7] = np.nan
