@@ -194,10 +194,11 @@ def test_linear_gemv_shapes(ex, fmt, shape, n):
 
 @pytest.mark.parametrize("fmt", [srq.Q8, srq.Q4, srq.F32])
 @pytest.mark.parametrize("n", [17, 32, 33, 64, 100, 256])
-@pytest.mark.parametrize("shape", [(640, 2048), (1000, 256), (300, 8192)])
+@pytest.mark.parametrize("shape", [(640, 2048), (1000, 256), (300, 8192), (301, 2048)])
 def test_linear_gemm_mfma(ex, fmt, n, shape):
     """32-row tiles (n <= 32) and 64-row tiles; K split into slices (narrow
-    outputs, long K) and whole-K tiles (K = 256)."""
+    outputs, long K) and whole-K tiles (K = 256); slice sums four outputs at a
+    time (rows % 4 == 0) or one (301 rows)."""
     print("gemm", fmt, n, shape, flush=True)
     rows, cols = shape
     rng = oracle.RNG(77 + n + cols)
