@@ -31,6 +31,7 @@ constexpr int kMaxHd = 256;
 // otherwise each pay the merge's cache write-back and invalidation.
 constexpr int kFusedRows = 4;
 constexpr int kFusedSplits = 16;  // splits of 64 positions: context <= 1024
+static_assert(kFusedSplits <= 64, "the fused kernel's one-wave merge holds one split per lane");
 
 __device__ __forceinline__ const float *kv_row(const RowMeta &m, int sess, int pos, int kvdim, int which) {
     const int page = m.pages[(int64_t)sess * m.pt_stride + pos / kPageTokens];
@@ -271,6 +272,43 @@ constexpr int kMergeChunk = 256;  // splits per pass of the weight table
 constexpr int kMergePairs = kMaxGroup * kMaxHd / 256;
 constexpr int kMergeBatch = 16;   // partial loads in flight per (head, dim) pair
 
+// Merge of at most 64 split partials for head h of a row by one wave, with no
+// barrier: the same arithmetic and order as merge_splits below (lane i holds
+// split i's factor; each lane's dims accumulate the splits in order).
+__device__ __forceinline__ void merge_wave(const AttnArgs &A, const float *part, int nsplit, int row, int h, int hd,
+                                           int used) {
+    const int lane = threadIdx.x & 63;
+    float M = -FLT_MAX;
+    if (lane < used) M = partial((float *)part, row, h, lane, A.heads, nsplit, hd)[0];
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
+    double l = 0.0;
+    float mi = 0.0f;
+    if (lane < used) {
+        const float *p = partial((float *)part, row, h, lane, A.heads, nsplit, hd);
+        mi = p[0];
+        l = *(const double *)(p + 2) * exp((double)mi - (double)M);
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) l += __shfl_xor(l, o, 64);
+    const double lse = (double)M + log(l);
+    const float cf = lane < used ? (float)exp((double)mi - lse) : 0.0f;
+    for (int j = lane; j < hd; j += 64) {
+        const float *pb = partial((float *)part, row, h, 0, A.heads, nsplit, hd) + 4 + j;
+        float o = 0.0f;
+        for (int i0 = 0; i0 < used; i0 += kMergeBatch) {
+            float v[kMergeBatch];
+#pragma unroll
+            for (int b = 0; b < kMergeBatch; ++b) v[b] = pb[(int64_t)min(i0 + b, used - 1) * (hd + 4)];
+#pragma unroll
+            for (int b = 0; b < kMergeBatch; ++b)
+                if (i0 + b < used)
+                    o = __builtin_fmaf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(cf), i0 + b)), v[b], o);
+        }
+        A.out[(int64_t)row * A.heads * hd + (int64_t)h * hd + j] = o;
+    }
+}
+
 // Merge of split partials (m_i, l_i, o_i) for heads h0 .. h0+nh-1 of a row,
 // by all 256 threads of the workgroup:
 //   M = max_i m_i, l = sum_i l_i exp(m_i - M) (FP64), lse = M + log(l),
@@ -352,8 +390,6 @@ __global__ __launch_bounds__(256) void attn_fused_kernel(const AttnArgs A, float
     __shared__ float qs[kMaxGroup * HD];
     __shared__ float sc[kMaxGroup][kSplit];
     __shared__ float4 red[KG][DG];
-    __shared__ float cf[kMaxGroup][kMergeChunk];
-    __shared__ double lse[kMaxGroup];
     __shared__ int last;
 
     const int row = blockIdx.x, kh = blockIdx.y, sp = blockIdx.z;
@@ -471,7 +507,8 @@ __global__ __launch_bounds__(256) void attn_fused_kernel(const AttnArgs A, float
     if (!last) return;
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     if (tid == 0) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    merge_splits(A, part, nsplit, row, kh * G, G, HD, used, cf, lse);
+    // used <= kFusedSplits <= 64: one wave per head merges on its own.
+    for (int g = wave; g < G; g += 4) merge_wave(A, part, nsplit, row, kh * G + g, HD, used);
 }
 
 // lse and the weighted sum of split partials for one (row, head).
