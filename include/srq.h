@@ -40,6 +40,9 @@ extern "C" {
 #define SRQ_ENONFINITE (-33) /* non-finite weight or logit                    */
 #define SRQ_ERANGE (-34)     /* KV cache context exhausted                    */
 #define SRQ_ECANCELED (-125) /* caller's cancel flag was set                  */
+#define SRQ_EFILE (-2)       /* archive file missing, unreadable or short     */
+#define SRQ_EFORMAT (-74)    /* archive metadata rejected (index, header,
+                              * names, shapes, dtypes, extents)              */
 
 typedef enum { SRQ_F32 = 0, SRQ_Q8 = 1, SRQ_Q4 = 2 } srq_format;
 typedef enum { SRQ_SRC_F32 = 0, SRQ_SRC_BF16 = 1, SRQ_SRC_F16 = 2 } srq_src_dtype;
@@ -167,6 +170,28 @@ int srq_model_resident_bytes(const srq_model *m, int64_t *bytes);
 int srq_model_weight(srq_model *m, int kind, int layer, srq_weight **out);
 /* The FP32 RoPE tables (M:5034-5043), [context x head_dim/2] each, host. */
 int srq_model_rope_tables(const srq_model *m, float *cos_out, float *sin_out);
+/* openHFArchiveFormat (M:648-850) + readParam / readTensorValues
+ * (M:855-920): load every tensor of m's profile from the Transformers
+ * archive in directory dir -- model.safetensors, or the shards that
+ * model.safetensors.index.json names -- converting F32 / F16 / BF16 values
+ * and packing them to m's format on the device.  The archive is checked as
+ * the reference checks it (index names and paths, at most 128 shards, file
+ * and header size limits, duplicate-free UTF-8 JSON headers, the profile's
+ * exact names and shapes from hfProfileSpecs M:426-440, dtype widths,
+ * exact extents, no gaps, overlaps or trailing bytes, nothing missing):
+ * failures are SRQ_EFORMAT (or SRQ_EFILE for I/O) and are found before any
+ * weight is written.  A non-finite value fails with SRQ_ENONFINITE and the
+ * tensor's name.  cancel (host, nullable) is polled between 16 MiB chunks
+ * (the reference's context check, M:894): SRQ_ECANCELED.  After any failure
+ * m holds partly loaded weights and should be destroyed.  source_bytes
+ * (nullable) receives the archive's total file size.  Files are read with
+ * pread through pinned staging; copies and packing overlap the reads. */
+int srq_model_load_safetensors(srq_model *m, const char *dir, const volatile int32_t *cancel,
+                               int64_t *source_bytes);
+/* The archive checks of srq_model_load_safetensors alone, on the host, for
+ * configuration c (no device, nothing allocated on a GPU): the reference
+ * inspects the metadata before any parameter storage exists (M:121-122). */
+int srq_archive_check(const srq_model_config *c, const char *dir, int64_t *source_bytes);
 
 /* ---- paged KV: pagePool / KVCache (M:5846-6062) ------------------------ */
 /* A pool owns max_pages device pages of 2*32*kvdim*layers floats, laid out

@@ -21,6 +21,7 @@ LIB_PATH = os.path.join(HERE, "libsrq.so")
 F32, Q8, Q4 = 0, 1, 2
 SRC_F32, SRC_BF16, SRC_F16 = 0, 1, 2
 OK, EDEVICE, ENOMEM, EINVAL, ENOSPC, ENONFINITE, ERANGE, ECANCELED = 0, -5, -12, -22, -28, -33, -34, -125
+EFILE, EFORMAT = -2, -74
 T_EMBED, T_FINAL_NORM, T_OUTPUT = 0, 1, 2
 T_ATTN_NORM, T_Q, T_K, T_V, T_O, T_FFN_NORM, T_GATE, T_UP, T_DOWN, T_Q_BIAS, T_K_BIAS, T_V_BIAS = range(10, 22)
 T_QKV, T_GATE_UP = 22, 23  # fused storage views (srq_model_weight only)
@@ -62,7 +63,8 @@ EXPORTS = [
     "srq_exec_stream", "srq_fill_normal", "srq_packed_bytes", "srq_pack", "srq_weight_create", "srq_weight_wrap",
     "srq_weight_destroy", "srq_weight_info", "srq_dequant_rows", "srq_linear", "srq_linear_enqueue", "srq_model_create",
     "srq_model_load", "srq_model_destroy", "srq_model_resident_bytes", "srq_model_weight",
-    "srq_model_rope_tables", "srq_pool_create", "srq_pool_destroy", "srq_cache_create", "srq_cache_destroy",
+    "srq_model_rope_tables", "srq_model_load_safetensors", "srq_archive_check",
+    "srq_pool_create", "srq_pool_destroy", "srq_cache_create", "srq_cache_destroy",
     "srq_cache_pos", "srq_cache_read", "srq_step", "srq_argmax", "srq_sample", "srq_decoder_create", "srq_decoder_run",
     "srq_decoder_tokens", "srq_decoder_destroy", "srq_generate_greedy",
 ]
@@ -100,6 +102,8 @@ def _declare(L):
         "srq_model_resident_bytes": (C.c_int, [P, C.POINTER(I64)]),
         "srq_model_weight": (C.c_int, [P, C.c_int, C.c_int, PP]),
         "srq_model_rope_tables": (C.c_int, [P, P, P]),
+        "srq_model_load_safetensors": (C.c_int, [P, C.c_char_p, P, C.POINTER(I64)]),
+        "srq_archive_check": (C.c_int, [C.POINTER(ModelConfig), C.c_char_p, C.POINTER(I64)]),
         "srq_pool_create": (C.c_int, [P, I32, PP]),
         "srq_pool_destroy": (C.c_int, [P]),
         "srq_cache_create": (C.c_int, [P, I32, PP]),
@@ -329,6 +333,16 @@ class Model:
 
     def load_device(self, kind, layer, ptr, dtype=SRC_F32):
         check(lib().srq_model_load(self.h, kind, layer, C.c_void_p(ptr), dtype))
+
+    def load_safetensors(self, directory, cancel=None):
+        """Every tensor of the profile from a Transformers archive directory
+        (model.safetensors or an indexed set of shards); returns the
+        archive's size in bytes.  cancel: an optional ctypes.c_int32 polled
+        between chunks."""
+        size = C.c_int64()
+        flag = C.byref(cancel) if cancel is not None else None
+        check(lib().srq_model_load_safetensors(self.h, os.fsencode(directory), flag, C.byref(size)))
+        return size.value
 
     def resident_bytes(self):
         b = C.c_int64()

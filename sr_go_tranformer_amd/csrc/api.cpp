@@ -672,13 +672,17 @@ int srq_model_weight(srq_model *m, int kind, int layer, srq_weight **out) {
     return SRQ_OK;
 }
 
-int srq_model_load(srq_model *m, int kind, int layer, const void *src, srq_src_dtype dtype) {
+}  // extern "C"
+
+namespace srq {
+// srq_model_load without the join: the convert/pack kernels are queued on
+// the executor's stream and a non-finite value sets error word 0.
+int model_load_enqueue(srq_model *m, int kind, int layer, const void *src, int dtype) {
     if (!m || !src) return fail(SRQ_EINVAL, "null pointer");
     if (dtype < SRQ_SRC_F32 || dtype > SRQ_SRC_F16) return fail(SRQ_EINVAL, "bad source dtype");
     srq_exec *e = m->e;
     DeviceGuard g(m->device);
     const int64_t d = m->c.dim, kd = m->kvdim;
-    int rc;
     float *vec = nullptr;
     int64_t count = 0;
     switch (kind) {
@@ -699,15 +703,27 @@ int srq_model_load(srq_model *m, int kind, int layer, const void *src, srq_src_d
             break;
         default: break;
     }
-    if (vec) {
-        rc = launch_convert_f32(e->stream, count, src, dtype, vec, e->d_err);
-    } else {
-        srq_weight *w = model_matrix(m, kind, layer);
-        if (!w) return fail(SRQ_EINVAL, "no tensor of kind %d at layer %d", kind, layer);
-        rc = fill_weight(e, *w, src, dtype);
-    }
-    SRQ_CHECK(rc);
-    return check_err_flag(e, SRQ_ENONFINITE, "non-finite HF weight");
+    if (vec) return launch_convert_f32(e->stream, count, src, dtype, vec, e->d_err);
+    srq_weight *w = model_matrix(m, kind, layer);
+    if (!w) return fail(SRQ_EINVAL, "no tensor of kind %d at layer %d", kind, layer);
+    return fill_weight(e, *w, src, dtype);
+}
+
+const srq_model_config &model_config(const srq_model *m) { return m->c; }
+int model_device(const srq_model *m) { return m->device; }
+hipStream_t model_stream(const srq_model *m) { return m->e->stream; }
+const int32_t *model_error_word(const srq_model *m) { return m->e->d_err; }
+int model_join_nonfinite(srq_model *m, const char *what) {
+    DeviceGuard g(m->device);
+    return check_err_flag(m->e, SRQ_ENONFINITE, what);
+}
+}  // namespace srq
+
+extern "C" {
+
+int srq_model_load(srq_model *m, int kind, int layer, const void *src, srq_src_dtype dtype) {
+    SRQ_CHECK(model_load_enqueue(m, kind, layer, src, dtype));
+    return model_join_nonfinite(m, "non-finite HF weight");
 }
 
 int srq_model_rope_tables(const srq_model *m, float *cos_out, float *sin_out) {

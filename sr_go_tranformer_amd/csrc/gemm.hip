@@ -35,7 +35,7 @@ namespace {
 constexpr int BN = 128, BK = 32, LDK = BK + 4;
 constexpr int kCUs = 256;          // MI355X compute units
 constexpr int kFillWGs = 512;      // two resident workgroups on each CU
-constexpr int kMinSliceSteps = 8;  // K steps per split-K slice (256 inputs)
+constexpr int kMinSliceInputs = 256;  // inputs per split-K slice, at least
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 template <int FMT>
@@ -666,7 +666,7 @@ GemmPlan plan_gemm(int fmt, int32_t n, int64_t rows, int64_t cols) {
     p.bm = n <= 32 ? 32 : 64;
     const int bn = p.x3 ? XBN : BN, bk = p.x3 ? kBlock : BK;
     const int64_t tiles = ((rows + bn - 1) / bn) * ((n + p.bm - 1) / p.bm);
-    const int ksteps = (int)(cols / bk), min_steps = 256 / bk;
+    const int ksteps = (int)(cols / bk), min_steps = kMinSliceInputs / bk;
     int slices = 1;
     if (tiles < kCUs) {
         const int64_t want = (kFillWGs + tiles - 1) / tiles;

@@ -172,4 +172,17 @@ int launch_attention(hipStream_t s, const AttnArgs &a, float *scratch, int32_t *
 size_t attention_scratch_bytes(int32_t n, int32_t heads, int32_t head_dim, int32_t max_len);
 int attention_prepare();
 
+// ----------------------------------------------------------- model hooks
+// For the archive loader.  model_load_enqueue is srq_model_load without the
+// join: it queues the convert/pack on the model's executor stream, and a
+// non-finite source value sets the executor's device error word 0, which
+// stays set until model_join_nonfinite (which joins the stream) clears it
+// and fails with SRQ_ENONFINITE and the message `what`.
+int model_load_enqueue(srq_model *m, int kind, int layer, const void *src, int dtype);
+int model_join_nonfinite(srq_model *m, const char *what);
+const srq_model_config &model_config(const srq_model *m);
+int model_device(const srq_model *m);
+hipStream_t model_stream(const srq_model *m);
+const int32_t *model_error_word(const srq_model *m);
+
 }  // namespace srq
