@@ -493,6 +493,100 @@ def bench_longctx_decode(srq, args):
     return 0
 
 
+def write_bf16_archive(directory, cfg, seed, shard_bytes=5 << 30):
+    """A Transformers directory of the given config.json dict whose tensors
+    are BF16 words of N(0, 0.02) values (a 32 Mi-word block repeated), in
+    shards of at most shard_bytes with an index.  Returns the archive size."""
+    rng = np.random.default_rng(seed)
+    block = (rng.normal(0.0, 0.02, 16 << 20).astype(np.float32).view(np.uint32) >> 16).astype("<u2").tobytes()
+    d, h, v, L = cfg["hidden_size"], cfg["intermediate_size"], cfg["vocab_size"], cfg["num_hidden_layers"]
+    kd = d // cfg["num_attention_heads"] * cfg["num_key_value_heads"]
+    specs = [("model.embed_tokens.weight", [v, d])]
+    for i in range(L):
+        p = "model.layers.%d." % i
+        specs += [(p + "input_layernorm.weight", [d]), (p + "self_attn.q_proj.weight", [d, d]),
+                  (p + "self_attn.k_proj.weight", [kd, d]), (p + "self_attn.v_proj.weight", [kd, d]),
+                  (p + "self_attn.o_proj.weight", [d, d]), (p + "post_attention_layernorm.weight", [d]),
+                  (p + "mlp.gate_proj.weight", [h, d]), (p + "mlp.up_proj.weight", [h, d]),
+                  (p + "mlp.down_proj.weight", [d, h])]
+    specs += [("model.norm.weight", [d]), ("lm_head.weight", [v, d])]
+    groups, cur, size = [], [], 0
+    for name, shape in specs:
+        n = 2 * int(np.prod(shape))
+        if cur and size + n > shard_bytes:
+            groups.append(cur)
+            cur, size = [], 0
+        cur.append((name, shape, n))
+        size += n
+    groups.append(cur)
+    with open(os.path.join(directory, "config.json"), "w") as f:
+        json.dump(cfg, f)
+    index, total = {}, 0
+    for i, group in enumerate(groups):
+        fname = "model-%05d-of-%05d.safetensors" % (i + 1, len(groups))
+        header, off = {}, 0
+        for name, shape, n in group:
+            header[name] = {"dtype": "BF16", "shape": shape, "data_offsets": [off, off + n]}
+            off += n
+            index[name] = fname
+        hb = json.dumps(header).encode()
+        with open(os.path.join(directory, fname), "wb") as f:
+            f.write(len(hb).to_bytes(8, "little") + hb)
+            left = off
+            while left > 0:
+                k = min(left, len(block))
+                f.write(block[:k])
+                left -= k
+        total += 8 + len(hb) + off
+        print("archive shard %d/%d written" % (i + 1, len(groups)), file=sys.stderr, flush=True)
+    with open(os.path.join(directory, "model.safetensors.index.json"), "w") as f:
+        json.dump({"weight_map": index}, f)
+    return total
+
+
+def bench_archive_load(srq, args):
+    """Load a Mistral-7B-shape BF16 Transformers archive (three ~5 GB shards
+    in the page cache) into a Q8 model: archive checks, pread into pinned
+    slots, copies and device packing (srq_model_load_safetensors)."""
+    import shutil
+    import tempfile
+    from sr_go_tranformer_amd import hf
+    cfg = {"architectures": ["MistralForCausalLM"], "model_type": "mistral", "vocab_size": 32768,
+           "hidden_size": 4096, "intermediate_size": 14336, "num_hidden_layers": 32, "num_attention_heads": 32,
+           "num_key_value_heads": 8, "max_position_embeddings": 32768, "rope_theta": 1000000.0,
+           "rms_norm_eps": 1e-5, "hidden_act": "silu", "tie_word_embeddings": False, "bos_token_id": 1,
+           "eos_token_id": 2, "sliding_window": None}
+    root = tempfile.mkdtemp(prefix="srq_archive_", dir=args.archive_dir)
+    try:
+        if shutil.disk_usage(root).free < 20e9:
+            print("need 20 GB free under %s for the archive" % root, file=sys.stderr)
+            return 2
+        size = write_bf16_archive(root, cfg, args.seed)
+        ex = srq.Executor(0)
+        times = []
+        for _ in range(3):
+            m, _ = hf.open_model(ex, root, "q8", context_limit=4096)
+            ex.synchronize()
+            m.close()
+            t0 = time.perf_counter()
+            m, _ = hf.open_model(ex, root, "q8", context_limit=4096)
+            ex.synchronize()
+            times.append(time.perf_counter() - t0)
+            m.close()
+        ex.close()
+    finally:
+        shutil.rmtree(root, ignore_errors=True)
+    best = min(times)
+    print(json.dumps({
+        "metric": "Mistral-7B-shape BF16 safetensors archive load to Q8 (GB/s of archive)",
+        "value": round(size / best / 1e9, 2), "unit": "GB/s", "n_gpus": 1, "higher_is_better": True,
+        "dtype": "bf16->q8", "data": "synthetic",
+        "config": {"workload": "Mistral-7B shape, 3 BF16 shards in the page cache, config.json read, archive "
+                               "checked, loaded and packed to Q8", "archive_bytes": size, "seed": args.seed},
+        "seconds": [round(t, 3) for t in times]}), flush=True)
+    return 0
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -505,7 +599,7 @@ def main():
     ap.add_argument("--config", default="mistral7b-q8-decode",
                     choices=["mistral7b-q8-decode", "smollm2-q8-decode", "llama1b-q8-gemv-sweep",
                              "mistral7b-q4mixed-prefill", "llama3b-q8-continuous-batching",
-                             "mistral7b-q8-longctx-decode"],
+                             "mistral7b-q8-longctx-decode", "mistral7b-bf16-archive-load"],
                     help="workload; the default is the headline Mistral-7B Q8 decode")
     ap.add_argument("--prompt-tokens", type=int, default=2048, help="mistral7b-q4mixed-prefill: prompt length")
     ap.add_argument("--gen-tokens", type=int, default=128,
@@ -516,6 +610,8 @@ def main():
     ap.add_argument("--gemv-only", action="store_true",
                     help="run only the GEMV roofline leg (standalone weights) and a calibration copy")
     ap.add_argument("--gemv-rows", type=int, default=28672, help="--gemv-only: weight rows (4096 columns)")
+    ap.add_argument("--archive-dir", default=None,
+                    help="mistral7b-bf16-archive-load: where the temporary archive is written (default: TMPDIR)")
     ap.add_argument("--eager", action="store_true",
                     help="launch each decode kernel directly instead of replaying the captured graph "
                          "(for kernel tracers that cannot follow graph launches)")
@@ -543,6 +639,8 @@ def main():
         return bench_continuous_batching(srq, args)
     if args.config == "mistral7b-q8-longctx-decode":
         return bench_longctx_decode(srq, args)
+    if args.config == "mistral7b-bf16-archive-load":
+        return bench_archive_load(srq, args)
 
     t_start = time.perf_counter()
     ex = srq.Executor(0)
