@@ -316,7 +316,7 @@ def bench_q4mixed_prefill(srq, args):
         hip.record(b, stream)
         chunk_ms.append(hip.elapsed_ms(a, b))
     first = int(model.argmax_last()[0])
-    dec = srq.Decoder(model, cache, first, gen - 1)
+    dec = srq.Decoder(model, cache, first, gen - 1, eager=args.eager)
     ex.synchronize()
     a, b = hip.create(), hip.create()
     hip.record(a, stream)
