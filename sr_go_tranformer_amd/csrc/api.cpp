@@ -881,11 +881,14 @@ int validate_step(srq_model *m, int32_t sessions, srq_cache *const *caches, cons
 struct StepMeta {
     int32_t *tokens, *pos, *sess, *pages, *sel, *expand;
     int32_t pt_stride;
+    int32_t *tiles = nullptr;  // query tiles {first row, rows} (AttnArgs::tiles)
+    int32_t ntiles = 0;
 };
 
-// Layout of the packed metadata buffer (device and pinned host mirror).
+// Layout of the packed metadata buffer (device and pinned host mirror): at
+// most n query tiles follow the per-session tables.
 size_t meta_words(int32_t n, int32_t sessions, int32_t pt_stride) {
-    return (size_t)n * 3 + (size_t)sessions * pt_stride + (size_t)sessions * 2;
+    return (size_t)n * 5 + (size_t)sessions * pt_stride + (size_t)sessions * 2;
 }
 
 StepMeta carve(int32_t *base, int32_t n, int32_t sessions, int32_t pt_stride) {
@@ -896,6 +899,7 @@ StepMeta carve(int32_t *base, int32_t n, int32_t sessions, int32_t pt_stride) {
     s.pages = base + 3 * n;
     s.sel = s.pages + (size_t)sessions * pt_stride;
     s.expand = s.sel + sessions;
+    s.tiles = s.expand + sessions;
     s.pt_stride = pt_stride;
     return s;
 }
@@ -980,6 +984,8 @@ int enqueue_layers(srq_exec *e, Workspace &ws, srq_model *m, srq_pool *pool, int
         at.head_dim = m->hd;
         at.max_len = max_len;
         at.meta = meta;
+        at.tiles = dm.tiles;
+        at.ntiles = dm.ntiles;
         SRQ_CHECK(launch_attention(e->stream, at, as<float>(ws.ATT), as<int32_t>(ws.ATTC)));
         // O projection + residual (M:6398-6400).
         SRQ_CHECK(run_linear(e, ws, L.o, A, n, X, d, nullptr, 0.0, X));
@@ -1079,8 +1085,14 @@ extern "C" int srq_step(srq_exec *e, srq_model *m, int32_t sessions, srq_cache *
     }
     StepMeta hm = carve(e->h_meta, n, sessions, pt_stride);
     std::vector<int32_t> last_rows(sessions);
-    int32_t r = 0;
+    int32_t r = 0, ntiles = 0;
     for (int32_t i = 0; i < sessions; ++i) {
+        // Query tiles: up to kAttnTileRows consecutive rows of this session.
+        for (int32_t t0 = 0; t0 < chunk_lens[i]; t0 += kAttnTileRows) {
+            hm.tiles[2 * ntiles] = r + t0;
+            hm.tiles[2 * ntiles + 1] = std::min<int32_t>(kAttnTileRows, chunk_lens[i] - t0);
+            ++ntiles;
+        }
         for (int32_t j = 0; j < chunk_lens[i]; ++j, ++r) {
             hm.tokens[r] = tokens[r];
             hm.pos[r] = caches[i]->pos + j;
@@ -1101,6 +1113,7 @@ extern "C" int srq_step(srq_exec *e, srq_model *m, int32_t sessions, srq_cache *
     }
     SRQ_HIP(hipMemcpyAsync(ws.meta.p, e->h_meta, words * 4, hipMemcpyHostToDevice, e->stream));
     StepMeta dm = carve(as<int32_t>(ws.meta), n, sessions, pt_stride);
+    dm.ntiles = ntiles;
 
     // Embedding rows (copyRow, M:6364-6375).
     SRQ_CHECK(launch_dequant_rows(e->stream, m->embed.fmt, m->c.dim, m->embed.values, m->embed.scales, dm.tokens, n,

@@ -16,6 +16,7 @@
 // combine kernel forms lse = M + log(sum_i l_i exp(m_i - M)) and
 // out = sum_i f32(exp(m_i - lse)) o_i, which equals the reference's
 // sum_s exp(score_s - lse) v_s up to f32 rounding of the factors.
+#include <algorithm>
 #include <cfloat>
 
 #include "srq_internal.h"
@@ -511,15 +512,191 @@ __global__ __launch_bounds__(256) void attn_fused_kernel(const AttnArgs A, float
     for (int g = wave; g < G; g += 4) merge_wave(A, part, nsplit, row, kh * G + g, HD, used);
 }
 
-// lse and the weighted sum of split partials for one (row, head).
+// lse and the weighted sum of split partials for one (row, head); split i
+// covers positions [i*split_len, (i+1)*split_len).
 __global__ __launch_bounds__(256) void attn_combine_kernel(const AttnArgs A, const float *__restrict__ part,
-                                                           int nsplit) {
+                                                           int nsplit, int split_len) {
     __shared__ float cf[kMaxGroup][kMergeChunk];
     __shared__ double lse[kMaxGroup];
     const int row = blockIdx.x, h = blockIdx.y;
     const int len = A.meta.pos[row] + 1;
-    const int used = min(nsplit, (len + kSplit - 1) / kSplit);
+    const int used = min(nsplit, (len + split_len - 1) / split_len);
     merge_splits(A, part, nsplit, row, h, 1, A.head_dim, used, cf, lse);
+}
+
+// ------------------------------------------------------------ prefill
+// Causal attention for prefill-sized steps on FP32 MFMA
+// (v_mfma_f32_16x16x4f32), flash style.  Workgroup (query tile, kv head,
+// key split): a tile is up to 16 consecutive rows of one session, whose
+// positions are consecutive.  Wave w takes query head kh*G + w for the
+// tile's rows (G > 4: a second pass over the keys for heads 4..7; waves past
+// G only stage), so every K/V row staged in LDS serves all the GQA group's
+// heads and all 16 rows -- the split kernel re-reads K/V per row.
+//  S^T = K Q^T per 16-key step: MFMA step s feeds lane group g = lane/16
+//  the head dims (HD/4)g + s, so a lane's q and K values are contiguous; the
+//  result gives lane l the scores S[q = l%16][key = 4(l/16) + r], r = 0..3.
+//  P V: those registers are P's A operand, MFMA step r taking keys
+//  4(l/16) + r; lane l then holds O[q = 4(l/16) + rr][dim = 16b + l%16].
+//  Per query row an online softmax: running max m (f32), FP64 sum l of
+//  f32 exp(s - m), O rescaled by f32 exp(m_old - m_new) when the max grows.
+// Scores are f32 dot(q, k) * f32(1/sqrt(hd)) as in attend (M:5293-5352);
+// the split's {m, l, o} feed attn_combine_kernel, split sp covering keys
+// [sp*ks, (sp+1)*ks).  K/V chunks of 64 keys are double buffered through
+// registers: the next chunk's loads are in flight during this chunk's MFMAs.
+constexpr int kFlashChunk = 32;   // keys staged in LDS per pass
+constexpr int kFlashFill = 512;   // workgroups the key splits aim for
+typedef float flashx4 __attribute__((ext_vector_type(4)));
+
+template <int HD>
+__global__ __launch_bounds__(256) void attn_flash_kernel(const AttnArgs A, float *__restrict__ part, int nsplit,
+                                                         int ks) {
+    constexpr int LDH = HD + 4;           // LDS row stride (floats)
+    constexpr int QF = HD / 4;            // q values per lane
+    constexpr int NB = HD / 16;           // 16-dim output blocks
+    constexpr int CH = kFlashChunk;
+    constexpr int D4 = HD / 4;            // float4 per K/V row
+    constexpr int LPT = CH * D4 / 256;    // float4 per thread per chunk (K and V each)
+    __shared__ __attribute__((aligned(16))) float Ks[CH * LDH];
+    __shared__ __attribute__((aligned(16))) float Vs[CH * LDH];
+
+    const int tile = blockIdx.x, kh = blockIdx.y, sp = blockIdx.z;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int li = lane & 15, gq = lane >> 4;
+    static_assert(kAttnTileRows == 16, "a query tile is one 16-row MFMA operand");
+    const int r0 = A.tiles[2 * tile], cnt = A.tiles[2 * tile + 1];
+    const int sess = A.meta.sess[r0], pos0 = A.meta.pos[r0];
+    const int kvdim = A.kv_heads * HD, G = A.heads / A.kv_heads;
+    const int k_lo = sp * ks, k_hi = min(k_lo + ks, pos0 + cnt);
+    if (k_lo >= k_hi) return;  // no row of the tile reaches this split
+    const float scale = (float)(1.0 / sqrt((double)HD));
+    const int32_t *pt = A.meta.pages + (int64_t)sess * A.meta.pt_stride;
+    const float *lbase = A.meta.kv_pool + (int64_t)A.meta.layer * 2 * kPageTokens * kvdim + (int64_t)kh * HD;
+
+    for (int g0 = 0; g0 < G; g0 += 4) {
+        // K/V chunk registers, indexed only by unrolled loops (native vector
+        // type: HIP's float4 struct copies would go through scratch).
+        flashx4 kr[LPT], vr[LPT];
+        const int g = g0 + wave;
+        const bool active = g < G;
+        const int h = kh * G + (active ? g : 0);
+        float qf[QF];
+        {
+            const float *qp = A.q + (int64_t)(r0 + min(li, cnt - 1)) * A.heads * HD + (int64_t)h * HD + QF * gq;
+#pragma unroll
+            for (int u = 0; u < QF; u += 4) {
+                const flashx4 t = *(const flashx4 *)(qp + u);
+                qf[u] = t[0], qf[u + 1] = t[1], qf[u + 2] = t[2], qf[u + 3] = t[3];
+            }
+        }
+        flashx4 o[NB];
+#pragma unroll
+        for (int b = 0; b < NB; ++b) o[b] = flashx4{0.f, 0.f, 0.f, 0.f};
+        float m = -FLT_MAX;
+        double l = 0.0;
+
+        {
+            const int NEXT = k_lo;
+#pragma unroll
+            for (int i = 0; i < LPT; ++i) {
+                const int f = tid + 256 * i, key = min(NEXT + f / D4, k_hi - 1), d4 = f % D4;
+                const float *row = lbase + (int64_t)pt[key / kPageTokens] * A.meta.page_elems +
+                                   (int64_t)(key % kPageTokens) * kvdim;
+                kr[i] = *(const flashx4 *)(row + 4 * d4);
+                vr[i] = *(const flashx4 *)(row + (int64_t)kPageTokens * kvdim + 4 * d4);
+            }
+        }
+        for (int c0 = k_lo; c0 < k_hi; c0 += CH) {
+            __syncthreads();  // the previous chunk's LDS reads are done
+#pragma unroll
+            for (int i = 0; i < LPT; ++i) {
+                const int f = tid + 256 * i, k = f / D4, d4 = f % D4;
+                *(flashx4 *)(Ks + k * LDH + 4 * d4) = kr[i];
+                *(flashx4 *)(Vs + k * LDH + 4 * d4) = vr[i];
+            }
+            __syncthreads();
+            // The next chunk (keys clamped to the split: past its end this
+            // re-reads the last key, unused).
+            {
+                const int NEXT = c0 + CH;
+#pragma unroll
+            for (int i = 0; i < LPT; ++i) {
+                const int f = tid + 256 * i, key = min(NEXT + f / D4, k_hi - 1), d4 = f % D4;
+                const float *row = lbase + (int64_t)pt[key / kPageTokens] * A.meta.page_elems +
+                                   (int64_t)(key % kPageTokens) * kvdim;
+                kr[i] = *(const flashx4 *)(row + 4 * d4);
+                vr[i] = *(const flashx4 *)(row + (int64_t)kPageTokens * kvdim + 4 * d4);
+            }
+            }
+            if (!active) continue;
+            for (int st = 0; st < CH; st += 16) {
+                if (c0 + st >= k_hi) break;
+                // ---- S^T = K Q^T for 16 keys ----
+                flashx4 s4 = {0.f, 0.f, 0.f, 0.f};
+                const float *kp = Ks + (st + li) * LDH + QF * gq;
+#pragma unroll
+                for (int u = 0; u < QF; u += 4) {
+                    const flashx4 kv = *(const flashx4 *)(kp + u);
+                    s4 = __builtin_amdgcn_mfma_f32_16x16x4f32(kv[0], qf[u], s4, 0, 0, 0);
+                    s4 = __builtin_amdgcn_mfma_f32_16x16x4f32(kv[1], qf[u + 1], s4, 0, 0, 0);
+                    s4 = __builtin_amdgcn_mfma_f32_16x16x4f32(kv[2], qf[u + 2], s4, 0, 0, 0);
+                    s4 = __builtin_amdgcn_mfma_f32_16x16x4f32(kv[3], qf[u + 3], s4, 0, 0, 0);
+                }
+                // ---- causal mask, online softmax of query row li ----
+                float sv[4], p[4];
+                bool ok[4];
+                float tm = -FLT_MAX;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int key = c0 + st + 4 * gq + r;
+                    ok[r] = key < k_hi && key <= pos0 + li;
+                    sv[r] = s4[r] * scale;
+                    if (ok[r]) tm = fmaxf(tm, sv[r]);
+                }
+                tm = fmaxf(tm, __shfl_xor(tm, 16, 64));
+                tm = fmaxf(tm, __shfl_xor(tm, 32, 64));
+                const float mn = fmaxf(m, tm);
+                const float alpha = expf(m - mn);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) p[r] = ok[r] ? expf(sv[r] - mn) : 0.0f;
+                double ps = (((double)p[0] + (double)p[1]) + (double)p[2]) + (double)p[3];
+                ps += __shfl_xor(ps, 16, 64);
+                ps += __shfl_xor(ps, 32, 64);
+                l = l * (double)alpha + ps;
+                m = mn;
+#pragma unroll
+                for (int rr = 0; rr < 4; ++rr) {
+                    const float a = __shfl(alpha, 4 * gq + rr, 64);
+#pragma unroll
+                    for (int b = 0; b < NB; ++b) o[b][rr] *= a;
+                }
+                // ---- O += P V ----
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const float *vp = Vs + (st + 4 * gq + r) * LDH + li;
+#pragma unroll
+                    for (int b = 0; b < NB; ++b)
+                        o[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(p[r], vp[16 * b], o[b], 0, 0, 0);
+                }
+            }
+        }
+        if (active) {
+            // {m, l} of row li (held by every lane group), o of rows 4*gq + rr.
+            if (gq == 0 && li < cnt && pos0 + li + 1 > k_lo) {
+                float *pp = partial(part, r0 + li, h, sp, A.heads, nsplit, HD);
+                pp[0] = m;
+                *(double *)(pp + 2) = l;
+            }
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) {
+                const int j = 4 * gq + rr;
+                if (j < cnt && pos0 + j + 1 > k_lo) {
+                    float *pp = partial(part, r0 + j, h, sp, A.heads, nsplit, HD) + 4 + li;
+#pragma unroll
+                    for (int b = 0; b < NB; ++b) pp[16 * b] = o[b][rr];
+                }
+            }
+        }
+    }
 }
 
 }  // namespace
@@ -539,6 +716,27 @@ int launch_attention(hipStream_t s, const AttnArgs &a, float *scratch, int32_t *
     if (nsplit > 1024) return fail(SRQ_EINVAL, "attention: %d positions exceed the split table", a.max_len);
     const dim3 grid(a.n, a.kv_heads, nsplit);
     const bool fast = a.head_dim == 128 || a.head_dim == 64;
+    if (fast && a.tiles && a.ntiles > 0 && a.n >= 32 && a.n >= 8 * a.ntiles) {
+        // Prefill-sized steps: MFMA flash tiles, key splits sized so the
+        // grid reaches about kFlashFill workgroups, then the combine.
+        const int64_t wgs = (int64_t)a.ntiles * a.kv_heads;
+        const int want = (int)std::max<int64_t>(1, (kFlashFill + wgs - 1) / wgs);
+        // Split lengths are multiples of kSplit, so there are never more
+        // splits than attention_scratch_bytes provides for.
+        int ks = (a.max_len + want - 1) / want;
+        ks = std::max(kSplit, (ks + kSplit - 1) / kSplit * kSplit);
+        const int fsplit = (a.max_len + ks - 1) / ks;
+        if (fsplit > nsplit) return fail(SRQ_EINVAL, "attention: %d key splits exceed the scratch's %d", fsplit, nsplit);
+        const dim3 fg(a.ntiles, a.kv_heads, fsplit);
+        if (a.head_dim == 128)
+            attn_flash_kernel<128><<<fg, 256, 0, s>>>(a, scratch, fsplit, ks);
+        else
+            attn_flash_kernel<64><<<fg, 256, 0, s>>>(a, scratch, fsplit, ks);
+        SRQ_HIP(hipGetLastError());
+        attn_combine_kernel<<<dim3(a.n, a.heads), 256, 0, s>>>(a, scratch, fsplit, ks);
+        SRQ_HIP(hipGetLastError());
+        return SRQ_OK;
+    }
     if (fast && a.n <= kFusedRows && nsplit <= kFusedSplits) {
         // Decode-sized batches at short context: one launch, the last split
         // merges.  Each split then publishes its partials with an agent-scope
@@ -558,7 +756,7 @@ int launch_attention(hipStream_t s, const AttnArgs &a, float *scratch, int32_t *
     else
         attn_split_kernel<<<grid, 256, 0, s>>>(a, scratch, nsplit);
     SRQ_HIP(hipGetLastError());
-    attn_combine_kernel<<<dim3(a.n, a.heads), 256, 0, s>>>(a, scratch, nsplit);
+    attn_combine_kernel<<<dim3(a.n, a.heads), 256, 0, s>>>(a, scratch, nsplit, kSplit);
     SRQ_HIP(hipGetLastError());
     return SRQ_OK;
 }

@@ -10,6 +10,7 @@ namespace srq {
 
 constexpr int kBlock = 64;       // q8Block (M:3793): scale block width
 constexpr int kPageTokens = 32;  // pageTokens (M:5846)
+constexpr int kAttnTileRows = 16;  // rows per query tile of a step (AttnArgs::tiles)
 constexpr int kWave = 64;
 
 // f32(MaxFloat32 / (2*64*127)) (M:4346-4354): above it a row takes the
@@ -164,6 +165,11 @@ struct AttnArgs {
     int32_t n, heads, kv_heads, head_dim;
     int32_t max_len;    // upper bound of pos+1 over rows (sizes LDS)
     RowMeta meta;
+    // Query tiles of a step (nullable): ntiles pairs {first row, rows} of at
+    // most 16 consecutive rows of one session, covering every row once.
+    // Prefill-sized steps use them for the MFMA flash kernel.
+    const int32_t *tiles;
+    int32_t ntiles;
 };
 // scratch: attention_scratch_bytes(n, heads, head_dim, max_len) bytes;
 // counters: n*heads int32, zero before the first launch (the kernels leave
