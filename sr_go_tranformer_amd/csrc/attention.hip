@@ -524,6 +524,18 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const AttnArgs A, con
     merge_splits(A, part, nsplit, row, h, 1, A.head_dim, used, cf, lse);
 }
 
+// The same for heads h0 .. h0+nh-1 of a row per workgroup (nh <= kMaxGroup):
+// fewer, fuller workgroups for prefill-sized steps.
+__global__ __launch_bounds__(256) void attn_combine_heads_kernel(const AttnArgs A, const float *__restrict__ part,
+                                                                 int nsplit, int split_len, int nh) {
+    __shared__ float cf[kMaxGroup][kMergeChunk];
+    __shared__ double lse[kMaxGroup];
+    const int row = blockIdx.x, h0 = blockIdx.y * nh;
+    const int len = A.meta.pos[row] + 1;
+    const int used = min(nsplit, (len + split_len - 1) / split_len);
+    merge_splits(A, part, nsplit, row, h0, nh, A.head_dim, used, cf, lse);
+}
+
 // ------------------------------------------------------------ prefill
 // Causal attention for prefill-sized steps on FP32 MFMA
 // (v_mfma_f32_16x16x4f32), flash style.  Workgroup (query tile, kv head,
@@ -628,51 +640,57 @@ __global__ __launch_bounds__(256) void attn_flash_kernel(const AttnArgs A, float
             }
             }
             if (!active) continue;
-            for (int st = 0; st < CH; st += 16) {
+            for (int st = 0; st < CH; st += 32) {
                 if (c0 + st >= k_hi) break;
-                // ---- S^T = K Q^T for 16 keys ----
-                flashx4 s4 = {0.f, 0.f, 0.f, 0.f};
-                const float *kp = Ks + (st + li) * LDH + QF * gq;
+                // ---- S^T = K Q^T for 32 keys: two independent 16-key chains ----
+                flashx4 sa = {0.f, 0.f, 0.f, 0.f}, sb = {0.f, 0.f, 0.f, 0.f};
+                const float *ka = Ks + (st + li) * LDH + QF * gq, *kb = ka + 16 * LDH;
 #pragma unroll
                 for (int u = 0; u < QF; u += 4) {
-                    const flashx4 kv = *(const flashx4 *)(kp + u);
-                    s4 = __builtin_amdgcn_mfma_f32_16x16x4f32(kv[0], qf[u], s4, 0, 0, 0);
-                    s4 = __builtin_amdgcn_mfma_f32_16x16x4f32(kv[1], qf[u + 1], s4, 0, 0, 0);
-                    s4 = __builtin_amdgcn_mfma_f32_16x16x4f32(kv[2], qf[u + 2], s4, 0, 0, 0);
-                    s4 = __builtin_amdgcn_mfma_f32_16x16x4f32(kv[3], qf[u + 3], s4, 0, 0, 0);
+                    const flashx4 va = *(const flashx4 *)(ka + u), vb = *(const flashx4 *)(kb + u);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        sa = __builtin_amdgcn_mfma_f32_16x16x4f32(va[e], qf[u + e], sa, 0, 0, 0);
+                        sb = __builtin_amdgcn_mfma_f32_16x16x4f32(vb[e], qf[u + e], sb, 0, 0, 0);
+                    }
                 }
                 // ---- causal mask, online softmax of query row li ----
-                float sv[4], p[4];
-                bool ok[4];
+                float sv[8], p[8];
+                bool ok[8];
                 float tm = -FLT_MAX;
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const int key = c0 + st + 4 * gq + r;
+                for (int r = 0; r < 8; ++r) {
+                    const int key = c0 + st + 16 * (r >> 2) + 4 * gq + (r & 3);
                     ok[r] = key < k_hi && key <= pos0 + li;
-                    sv[r] = s4[r] * scale;
+                    sv[r] = (r < 4 ? sa[r & 3] : sb[r & 3]) * scale;
                     if (ok[r]) tm = fmaxf(tm, sv[r]);
                 }
                 tm = fmaxf(tm, __shfl_xor(tm, 16, 64));
                 tm = fmaxf(tm, __shfl_xor(tm, 32, 64));
                 const float mn = fmaxf(m, tm);
                 const float alpha = expf(m - mn);
+                double ps = 0.0;
 #pragma unroll
-                for (int r = 0; r < 4; ++r) p[r] = ok[r] ? expf(sv[r] - mn) : 0.0f;
-                double ps = (((double)p[0] + (double)p[1]) + (double)p[2]) + (double)p[3];
+                for (int r = 0; r < 8; ++r) {
+                    p[r] = ok[r] ? expf(sv[r] - mn) : 0.0f;
+                    ps += (double)p[r];
+                }
                 ps += __shfl_xor(ps, 16, 64);
                 ps += __shfl_xor(ps, 32, 64);
                 l = l * (double)alpha + ps;
                 m = mn;
+                if (__any(alpha != 1.0f)) {  // some row's max grew: rescale O
 #pragma unroll
-                for (int rr = 0; rr < 4; ++rr) {
-                    const float a = __shfl(alpha, 4 * gq + rr, 64);
+                    for (int rr = 0; rr < 4; ++rr) {
+                        const float a = __shfl(alpha, 4 * gq + rr, 64);
 #pragma unroll
-                    for (int b = 0; b < NB; ++b) o[b][rr] *= a;
+                        for (int b = 0; b < NB; ++b) o[b][rr] *= a;
+                    }
                 }
-                // ---- O += P V ----
+                // ---- O += P V (keys st + 16*half + 4*gq + r at MFMA step r) ----
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const float *vp = Vs + (st + 4 * gq + r) * LDH + li;
+                for (int r = 0; r < 8; ++r) {
+                    const float *vp = Vs + (st + 16 * (r >> 2) + 4 * gq + (r & 3)) * LDH + li;
 #pragma unroll
                     for (int b = 0; b < NB; ++b)
                         o[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(p[r], vp[16 * b], o[b], 0, 0, 0);
@@ -733,7 +751,9 @@ int launch_attention(hipStream_t s, const AttnArgs &a, float *scratch, int32_t *
         else
             attn_flash_kernel<64><<<fg, 256, 0, s>>>(a, scratch, fsplit, ks);
         SRQ_HIP(hipGetLastError());
-        attn_combine_kernel<<<dim3(a.n, a.heads), 256, 0, s>>>(a, scratch, fsplit, ks);
+        int nh = std::min(kMaxGroup, a.heads);
+        while (a.heads % nh) --nh;
+        attn_combine_heads_kernel<<<dim3(a.n, a.heads / nh), 256, 0, s>>>(a, scratch, fsplit, ks, nh);
         SRQ_HIP(hipGetLastError());
         return SRQ_OK;
     }
