@@ -279,11 +279,20 @@ RowMeta make_meta(srq_exec *e, srq_model *m, int layer, int32_t pt_stride, const
     return r;
 }
 
+// Rows above which srq_linear takes the MFMA GEMM: up to here a row's bits
+// do not depend on the batch (the GEMV computes rows independently).
+constexpr int32_t kLinearGemmRows = 16;
+// Rows above which a step's layers take the MFMA GEMM (with separate norm,
+// RoPE and SwiGLU kernels): from 9 rows the GEMV would stream every weight
+// twice (8 rows per pass).  Continuous-batching steps of 9-16 rows run
+// 14% faster this way (Llama-3.2-3B shape, 32 sessions).
+constexpr int32_t kStepGemmRows = 8;
+
 // y[n x w.rows] = x . W^T for n rows through the GEMV (chunks of 8) or the
-// MFMA GEMM (n > 16, K multiple of 32), with optional fused RMSNorm.
+// MFMA GEMM (n > gemm_rows, K multiple of 32), with optional fused RMSNorm.
 int run_linear(srq_exec *e, Workspace &ws, const srq_weight &w, const float *x, int32_t n, float *y, int64_t y_stride,
-               const float *norm_w, double eps, const float *residual) {
-    if (n > 16 && gemm_ok(w.fmt, w.cols) && !norm_w) {
+               const float *norm_w, double eps, const float *residual, int32_t gemm_rows = kLinearGemmRows) {
+    if (n > gemm_rows && gemm_ok(w.fmt, w.cols) && !norm_w) {
         SRQ_CHECK(ensure(ws.flags, gemm_scratch_bytes(w.fmt, n, w.rows, w.cols), e->stream));
         GemmArgs g{w.fmt, w.values, w.scales, w.rows, w.cols, x, n, y, y_stride, residual};
         return launch_gemm(e->stream, g, ws.flags.p, ws.flags.n);
@@ -924,7 +933,7 @@ int enqueue_layers(srq_exec *e, Workspace &ws, srq_model *m, srq_pool *pool, int
     const int64_t d = c.dim, kd = m->kvdim, H = c.hidden;
     float *X = as<float>(ws.X), *N = as<float>(ws.N), *Q = as<float>(ws.Q), *A = as<float>(ws.A);
     float *Hh = as<float>(ws.H), *W2 = as<float>(ws.W2);
-    const bool use_gemm = n > 16 && gemm_ok(m->L[0].qkv.fmt, d) && gemm_ok(m->L[0].down.fmt, H);
+    const bool use_gemm = n > kStepGemmRows && gemm_ok(m->L[0].qkv.fmt, d) && gemm_ok(m->L[0].down.fmt, H);
     int64_t *kvoff = nullptr;
     float *rope_cs = nullptr;
     if (!use_gemm) {
@@ -972,7 +981,7 @@ int enqueue_layers(srq_exec *e, Workspace &ws, srq_model *m, srq_pool *pool, int
             }
         } else {
             SRQ_CHECK(launch_rmsnorm(e->stream, X, L.n1, N, n, (int32_t)d, c.norm_eps));
-            SRQ_CHECK(run_linear(e, ws, L.qkv, N, n, W2, d + 2 * kd, nullptr, 0.0, nullptr));
+            SRQ_CHECK(run_linear(e, ws, L.qkv, N, n, W2, d + 2 * kd, nullptr, 0.0, nullptr, kStepGemmRows));
             SRQ_CHECK(launch_rope_kv(e->stream, W2, L.bias, n, (int32_t)d, (int32_t)kd, m->hd, m->cos_t, m->sin_t, Q, meta));
         }
         AttnArgs at{};
@@ -988,7 +997,7 @@ int enqueue_layers(srq_exec *e, Workspace &ws, srq_model *m, srq_pool *pool, int
         at.ntiles = dm.ntiles;
         SRQ_CHECK(launch_attention(e->stream, at, as<float>(ws.ATT), as<int32_t>(ws.ATTC)));
         // O projection + residual (M:6398-6400).
-        SRQ_CHECK(run_linear(e, ws, L.o, A, n, X, d, nullptr, 0.0, X));
+        SRQ_CHECK(run_linear(e, ws, L.o, A, n, X, d, nullptr, 0.0, X, kStepGemmRows));
         if (!use_gemm) {
             for (int32_t r0 = 0; r0 < n; r0 += nbg) {
                 GemvArgs a{};
@@ -1009,11 +1018,11 @@ int enqueue_layers(srq_exec *e, Workspace &ws, srq_model *m, srq_pool *pool, int
             }
         } else {
             SRQ_CHECK(launch_rmsnorm(e->stream, X, L.n2, N, n, (int32_t)d, c.norm_eps));
-            SRQ_CHECK(run_linear(e, ws, L.gu, N, n, W2, 2 * H, nullptr, 0.0, nullptr));
+            SRQ_CHECK(run_linear(e, ws, L.gu, N, n, W2, 2 * H, nullptr, 0.0, nullptr, kStepGemmRows));
             SRQ_CHECK(launch_swiglu(e->stream, W2, n, (int32_t)H, Hh));
         }
         // down + residual (M:6415-6417).
-        SRQ_CHECK(run_linear(e, ws, L.down, Hh, n, X, d, nullptr, 0.0, X));
+        SRQ_CHECK(run_linear(e, ws, L.down, Hh, n, X, d, nullptr, 0.0, X, kStepGemmRows));
     }
     return SRQ_OK;
 }
