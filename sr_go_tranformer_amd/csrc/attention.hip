@@ -163,7 +163,7 @@ __global__ __launch_bounds__(256) void attn_split_fast_kernel(const AttnArgs A, 
     constexpr int KPG = kSplit / KG;     // keys per value thread
     __shared__ float qs[kMaxGroup * HD];
     __shared__ float sc[kMaxGroup][kSplit];
-    __shared__ float4 red[KG][DG];
+    __shared__ float4 red[KG][kMaxGroup][DG];
 
     const int row = blockIdx.x, kh = blockIdx.y, sp = blockIdx.z;
     const int tid = threadIdx.x, lane = tid & 63;
@@ -243,29 +243,38 @@ __global__ __launch_bounds__(256) void attn_split_fast_kernel(const AttnArgs A, 
         const int sk = s < ns ? s : 0;
         vr[i] = ((const float4 *)(kv_row(A.meta, sess, s0 + sk, kvdim, 1) + (int64_t)kh * HD))[dg];
     }
-    for (int g = 0; g < G; ++g) {
-        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    // ---- values: every head of the group at once, one tree ------------------
+    {
+        float4 acc[kMaxGroup];
+#pragma unroll
+        for (int g = 0; g < kMaxGroup; ++g) acc[g] = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
         for (int i = 0; i < KPG; ++i) {
             const int s = kg + KG * i;
-            const float w = s < ns ? sc[g][s] : 0.0f;
-            acc.x = __builtin_fmaf(w, vr[i].x, acc.x);
-            acc.y = __builtin_fmaf(w, vr[i].y, acc.y);
-            acc.z = __builtin_fmaf(w, vr[i].z, acc.z);
-            acc.w = __builtin_fmaf(w, vr[i].w, acc.w);
-        }
-        red[kg][dg] = acc;
-        __syncthreads();
-        if (tid < DG) {
-            float4 t = red[0][tid];
-            for (int k2 = 1; k2 < KG; ++k2) {
-                const float4 u = red[k2][tid];
-                t.x += u.x, t.y += u.y, t.z += u.z, t.w += u.w;
+#pragma unroll
+            for (int g = 0; g < kMaxGroup; ++g) {
+                if (g >= G) break;
+                const float w = s < ns ? sc[g][s] : 0.0f;
+                acc[g].x = __builtin_fmaf(w, vr[i].x, acc[g].x);
+                acc[g].y = __builtin_fmaf(w, vr[i].y, acc[g].y);
+                acc[g].z = __builtin_fmaf(w, vr[i].z, acc[g].z);
+                acc[g].w = __builtin_fmaf(w, vr[i].w, acc[g].w);
             }
-            float *p = partial(part, row, kh * G + g, sp, A.heads, nsplit, HD);
-            ((float4 *)(p + 4))[tid] = t;
         }
-        __syncthreads();
+#pragma unroll
+        for (int g = 0; g < kMaxGroup; ++g)
+            if (g < G) red[kg][g][dg] = acc[g];
+    }
+    __syncthreads();
+    for (int t = tid; t < G * DG; t += 256) {
+        const int g = t / DG, j = t - g * DG;
+        float4 o = red[0][g][j];
+        for (int k2 = 1; k2 < KG; ++k2) {
+            const float4 u = red[k2][g][j];
+            o.x += u.x, o.y += u.y, o.z += u.z, o.w += u.w;
+        }
+        float *p = partial(part, row, kh * G + g, sp, A.heads, nsplit, HD);
+        ((float4 *)(p + 4))[j] = o;
     }
 }
 
@@ -278,33 +287,55 @@ constexpr int kMergeBatch = 16;   // partial loads in flight per (head, dim) pai
 // split i's factor; each lane's dims accumulate the splits in order).
 __device__ __forceinline__ void merge_wave(const AttnArgs &A, const float *part, int nsplit, int row, int h, int hd,
                                            int used) {
+    // One round of loads: every split's {m, l} (lane = split) and, for
+    // used <= kMergeBatch, the o values of this lane's first two dims.
     const int lane = threadIdx.x & 63;
-    float M = -FLT_MAX;
-    if (lane < used) M = partial((float *)part, row, h, lane, A.heads, nsplit, hd)[0];
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
-    double l = 0.0;
+    const float *pb = partial((float *)part, row, h, 0, A.heads, nsplit, hd) + 4;
     float mi = 0.0f;
+    double li = 0.0;
     if (lane < used) {
         const float *p = partial((float *)part, row, h, lane, A.heads, nsplit, hd);
         mi = p[0];
-        l = *(const double *)(p + 2) * exp((double)mi - (double)M);
+        li = *(const double *)(p + 2);
     }
+    float v0[kMergeBatch], v1[kMergeBatch];
+    const bool pre = used <= kMergeBatch;
+    if (pre) {
+        const int j0 = min(lane, hd - 1), j1 = min(lane + 64, hd - 1);
+#pragma unroll
+        for (int b = 0; b < kMergeBatch; ++b) {
+            const int64_t off = (int64_t)min(b, used - 1) * (hd + 4);
+            v0[b] = pb[off + j0];
+            v1[b] = pb[off + j1];
+        }
+    }
+    float M = lane < used ? mi : -FLT_MAX;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
+    double l = lane < used ? li * exp((double)mi - (double)M) : 0.0;
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) l += __shfl_xor(l, o, 64);
     const double lse = (double)M + log(l);
     const float cf = lane < used ? (float)exp((double)mi - lse) : 0.0f;
     for (int j = lane; j < hd; j += 64) {
-        const float *pb = partial((float *)part, row, h, 0, A.heads, nsplit, hd) + 4 + j;
         float o = 0.0f;
-        for (int i0 = 0; i0 < used; i0 += kMergeBatch) {
-            float v[kMergeBatch];
-#pragma unroll
-            for (int b = 0; b < kMergeBatch; ++b) v[b] = pb[(int64_t)min(i0 + b, used - 1) * (hd + 4)];
+        if (pre && j < lane + 128) {
+            const float *v = j == lane ? v0 : v1;
 #pragma unroll
             for (int b = 0; b < kMergeBatch; ++b)
-                if (i0 + b < used)
-                    o = __builtin_fmaf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(cf), i0 + b)), v[b], o);
+                if (b < used)
+                    o = __builtin_fmaf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(cf), b)), v[b], o);
+        } else {
+            for (int i0 = 0; i0 < used; i0 += kMergeBatch) {
+                float v[kMergeBatch];
+#pragma unroll
+                for (int b = 0; b < kMergeBatch; ++b) v[b] = pb[(int64_t)min(i0 + b, used - 1) * (hd + 4) + j];
+#pragma unroll
+                for (int b = 0; b < kMergeBatch; ++b)
+                    if (i0 + b < used)
+                        o = __builtin_fmaf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(cf), i0 + b)), v[b],
+                                           o);
+            }
         }
         A.out[(int64_t)row * A.heads * hd + (int64_t)h * hd + j] = o;
     }
@@ -390,7 +421,7 @@ __global__ __launch_bounds__(256) void attn_fused_kernel(const AttnArgs A, float
     constexpr int KPG = kSplit / KG;  // keys per value thread
     __shared__ float qs[kMaxGroup * HD];
     __shared__ float sc[kMaxGroup][kSplit];
-    __shared__ float4 red[KG][DG];
+    __shared__ float4 red[KG][kMaxGroup][DG];
     __shared__ int last;
 
     const int row = blockIdx.x, kh = blockIdx.y, sp = blockIdx.z;
@@ -473,30 +504,38 @@ __global__ __launch_bounds__(256) void attn_fused_kernel(const AttnArgs A, float
     }
     __syncthreads();
 
-    // ---- values ------------------------------------------------------------
-    for (int g = 0; g < G; ++g) {
-        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    // ---- values: every head of the group at once, one tree ------------------
+    {
+        float4 acc[kMaxGroup];
+#pragma unroll
+        for (int g = 0; g < kMaxGroup; ++g) acc[g] = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
         for (int i = 0; i < KPG; ++i) {
             const int sv = kg + KG * i;
-            const float w = sv < ns ? sc[g][sv] : 0.0f;
-            acc.x = __builtin_fmaf(w, vr[i].x, acc.x);
-            acc.y = __builtin_fmaf(w, vr[i].y, acc.y);
-            acc.z = __builtin_fmaf(w, vr[i].z, acc.z);
-            acc.w = __builtin_fmaf(w, vr[i].w, acc.w);
-        }
-        red[kg][dg] = acc;
-        __syncthreads();
-        if (tid < DG) {
-            float4 t = red[0][tid];
-            for (int k2 = 1; k2 < KG; ++k2) {
-                const float4 u = red[k2][tid];
-                t.x += u.x, t.y += u.y, t.z += u.z, t.w += u.w;
+#pragma unroll
+            for (int g = 0; g < kMaxGroup; ++g) {
+                if (g >= G) break;
+                const float w = sv < ns ? sc[g][sv] : 0.0f;
+                acc[g].x = __builtin_fmaf(w, vr[i].x, acc[g].x);
+                acc[g].y = __builtin_fmaf(w, vr[i].y, acc[g].y);
+                acc[g].z = __builtin_fmaf(w, vr[i].z, acc[g].z);
+                acc[g].w = __builtin_fmaf(w, vr[i].w, acc[g].w);
             }
-            float *p = partial(part, row, kh * G + g, sp, A.heads, nsplit, HD);
-            ((float4 *)(p + 4))[tid] = t;
         }
-        __syncthreads();
+#pragma unroll
+        for (int g = 0; g < kMaxGroup; ++g)
+            if (g < G) red[kg][g][dg] = acc[g];
+    }
+    __syncthreads();
+    for (int t = tid; t < G * DG; t += 256) {
+        const int g = t / DG, j = t - g * DG;
+        float4 o = red[0][g][j];
+        for (int k2 = 1; k2 < KG; ++k2) {
+            const float4 u = red[k2][g][j];
+            o.x += u.x, o.y += u.y, o.z += u.z, o.w += u.w;
+        }
+        float *p = partial(part, row, kh * G + g, sp, A.heads, nsplit, HD);
+        ((float4 *)(p + 4))[j] = o;
     }
 
     // ---- the last split of (row, kv head) merges ------------------------------
