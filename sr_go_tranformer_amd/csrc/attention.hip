@@ -178,21 +178,36 @@ __global__ __launch_bounds__(256) void attn_split_fast_kernel(const AttnArgs A, 
         }
         return;
     }
+    // Every K and V load of the split at once (one round of memory latency).
+    const int part4 = tid & 3;
+    float4 kr[QD / 4];
+    {
+        const int s = tid >> 2, sk = s < ns ? s : 0;  // clamp: load a valid row, drop below
+        const float *k = kv_row(A.meta, sess, s0 + sk, kvdim, 0) + (int64_t)kh * HD + part4 * QD;
+#pragma unroll
+        for (int u = 0; u < QD / 4; ++u) kr[u] = ((const float4 *)k)[u];
+    }
+    const int dg = tid % DG, kg = tid / DG;
+    float4 vr[KPG];
+#pragma unroll
+    for (int i = 0; i < KPG; ++i) {
+        const int s = kg + KG * i;
+        const int sk = s < ns ? s : 0;
+        vr[i] = ((const float4 *)(kv_row(A.meta, sess, s0 + sk, kvdim, 1) + (int64_t)kh * HD))[dg];
+    }
     for (int i = tid; i < G * HD; i += 256) {
         const int g = i / HD, j = i - g * HD;
         qs[i] = A.q[(int64_t)row * A.heads * HD + (int64_t)(kh * G + g) * HD + j];
     }
+    // Keep the V loads ahead of the barrier (the compiler would sink them).
+#pragma unroll
+    for (int i = 0; i < KPG; ++i) asm volatile("" ::"v"(vr[i].x), "v"(vr[i].y), "v"(vr[i].z), "v"(vr[i].w));
     __syncthreads();
     const float scale = (float)(1.0 / sqrt((double)HD));
 
     // ---- scores -------------------------------------------------------------
     {
-        const int s = tid >> 2, part4 = tid & 3;
-        const int sk = s < ns ? s : 0;  // clamp: load a valid row, drop below
-        const float *k = kv_row(A.meta, sess, s0 + sk, kvdim, 0) + (int64_t)kh * HD + part4 * QD;
-        float4 kr[QD / 4];
-#pragma unroll
-        for (int u = 0; u < QD / 4; ++u) kr[u] = ((const float4 *)k)[u];
+        const int s = tid >> 2;
 #pragma unroll
         for (int g = 0; g < kMaxGroup; ++g) {
             if (g >= G) break;
@@ -234,31 +249,29 @@ __global__ __launch_bounds__(256) void attn_split_fast_kernel(const AttnArgs A, 
     }
     __syncthreads();
 
-    // ---- values ------------------------------------------------------------
-    const int dg = tid % DG, kg = tid / DG;
-    float4 vr[KPG];
-#pragma unroll
-    for (int i = 0; i < KPG; ++i) {
-        const int s = kg + KG * i;
-        const int sk = s < ns ? s : 0;
-        vr[i] = ((const float4 *)(kv_row(A.meta, sess, s0 + sk, kvdim, 1) + (int64_t)kh * HD))[dg];
-    }
     // ---- values: every head of the group at once, one tree ------------------
     {
         float4 acc[kMaxGroup];
 #pragma unroll
         for (int g = 0; g < kMaxGroup; ++g) acc[g] = make_float4(0.f, 0.f, 0.f, 0.f);
+        // Per head: its KPG weights are read from LDS together, then the
+        // FMAs (keys in order, as the reduction below expects).
 #pragma unroll
-        for (int i = 0; i < KPG; ++i) {
-            const int s = kg + KG * i;
+        for (int g = 0; g < kMaxGroup; ++g) {
+            if (g < G) {
+                float w[KPG];
 #pragma unroll
-            for (int g = 0; g < kMaxGroup; ++g) {
-                if (g >= G) break;
-                const float w = s < ns ? sc[g][s] : 0.0f;
-                acc[g].x = __builtin_fmaf(w, vr[i].x, acc[g].x);
-                acc[g].y = __builtin_fmaf(w, vr[i].y, acc[g].y);
-                acc[g].z = __builtin_fmaf(w, vr[i].z, acc[g].z);
-                acc[g].w = __builtin_fmaf(w, vr[i].w, acc[g].w);
+                for (int i = 0; i < KPG; ++i) {
+                    const int s = kg + KG * i;
+                    w[i] = s < ns ? sc[g][s] : 0.0f;
+                }
+#pragma unroll
+                for (int i = 0; i < KPG; ++i) {
+                    acc[g].x = __builtin_fmaf(w[i], vr[i].x, acc[g].x);
+                    acc[g].y = __builtin_fmaf(w[i], vr[i].y, acc[g].y);
+                    acc[g].z = __builtin_fmaf(w[i], vr[i].z, acc[g].z);
+                    acc[g].w = __builtin_fmaf(w[i], vr[i].w, acc[g].w);
+                }
             }
         }
 #pragma unroll
@@ -461,6 +474,11 @@ __global__ __launch_bounds__(256) void attn_fused_kernel(const AttnArgs A, float
         const int g = i / HD, j = i - g * HD;
         qs[i] = A.q[(int64_t)row * A.heads * HD + (int64_t)(kh * G + g) * HD + j];
     }
+    // The V rows are consumed only after the softmax; without this the
+    // compiler sinks their loads past the barrier, which then costs a second
+    // round of memory latency instead of overlapping the K loads.
+#pragma unroll
+    for (int i = 0; i < KPG; ++i) asm volatile("" ::"v"(vr[i].x), "v"(vr[i].y), "v"(vr[i].z), "v"(vr[i].w));
     __syncthreads();
     const float scale = (float)(1.0 / sqrt((double)HD));
 
@@ -509,17 +527,24 @@ __global__ __launch_bounds__(256) void attn_fused_kernel(const AttnArgs A, float
         float4 acc[kMaxGroup];
 #pragma unroll
         for (int g = 0; g < kMaxGroup; ++g) acc[g] = make_float4(0.f, 0.f, 0.f, 0.f);
+        // Per head: its KPG weights are read from LDS together, then the
+        // FMAs (keys in order, as the reduction below expects).
 #pragma unroll
-        for (int i = 0; i < KPG; ++i) {
-            const int sv = kg + KG * i;
+        for (int g = 0; g < kMaxGroup; ++g) {
+            if (g < G) {
+                float w[KPG];
 #pragma unroll
-            for (int g = 0; g < kMaxGroup; ++g) {
-                if (g >= G) break;
-                const float w = sv < ns ? sc[g][sv] : 0.0f;
-                acc[g].x = __builtin_fmaf(w, vr[i].x, acc[g].x);
-                acc[g].y = __builtin_fmaf(w, vr[i].y, acc[g].y);
-                acc[g].z = __builtin_fmaf(w, vr[i].z, acc[g].z);
-                acc[g].w = __builtin_fmaf(w, vr[i].w, acc[g].w);
+                for (int i = 0; i < KPG; ++i) {
+                    const int sv = kg + KG * i;
+                    w[i] = sv < ns ? sc[g][sv] : 0.0f;
+                }
+#pragma unroll
+                for (int i = 0; i < KPG; ++i) {
+                    acc[g].x = __builtin_fmaf(w[i], vr[i].x, acc[g].x);
+                    acc[g].y = __builtin_fmaf(w[i], vr[i].y, acc[g].y);
+                    acc[g].z = __builtin_fmaf(w[i], vr[i].z, acc[g].z);
+                    acc[g].w = __builtin_fmaf(w[i], vr[i].w, acc[g].w);
+                }
             }
         }
 #pragma unroll
