@@ -294,7 +294,7 @@ int run_linear(srq_exec *e, Workspace &ws, const srq_weight &w, const float *x, 
                const float *norm_w, double eps, const float *residual, int32_t gemm_rows = kLinearGemmRows) {
     if (n > gemm_rows && gemm_ok(w.fmt, w.cols) && !norm_w) {
         SRQ_CHECK(ensure(ws.flags, gemm_scratch_bytes(w.fmt, n, w.rows, w.cols), e->stream));
-        GemmArgs g{w.fmt, w.values, w.scales, w.rows, w.cols, x, n, y, y_stride, residual};
+        GemmArgs g{w.fmt, w.values, w.scales, w.rows, w.cols, x, n, y, y_stride, residual, nullptr};
         return launch_gemm(e->stream, g, ws.flags.p, ws.flags.n);
     }
     const int nb = gemv_max_rows(w.fmt, w.cols, norm_w != nullptr, 0);
@@ -1018,8 +1018,11 @@ int enqueue_layers(srq_exec *e, Workspace &ws, srq_model *m, srq_pool *pool, int
             }
         } else {
             SRQ_CHECK(launch_rmsnorm(e->stream, X, L.n2, N, n, (int32_t)d, c.norm_eps));
-            SRQ_CHECK(run_linear(e, ws, L.gu, N, n, W2, 2 * H, nullptr, 0.0, nullptr, kStepGemmRows));
-            SRQ_CHECK(launch_swiglu(e->stream, W2, n, (int32_t)H, Hh));
+            // gate/up GEMM with SwiGLU in its split-K reduction (W2 is only
+            // a temporary when K is not split).
+            SRQ_CHECK(ensure(ws.flags, gemm_scratch_bytes(L.gu.fmt, n, L.gu.rows, L.gu.cols), e->stream));
+            GemmArgs g{L.gu.fmt, L.gu.values, L.gu.scales, L.gu.rows, L.gu.cols, N, n, W2, 2 * H, nullptr, Hh};
+            SRQ_CHECK(launch_gemm(e->stream, g, ws.flags.p, ws.flags.n));
         }
         // down + residual (M:6415-6417).
         SRQ_CHECK(run_linear(e, ws, L.down, Hh, n, X, d, nullptr, 0.0, X, kStepGemmRows));

@@ -652,6 +652,48 @@ __global__ __launch_bounds__(256) void gemm_reduce4_kernel(const GemmArgs G, con
     *(float4 *)(G.y + m * G.y_stride + j) = v;
 }
 
+// Sum of column j's K slices for row m, in slice order (as gemm_reduce_kernel).
+__device__ __forceinline__ float4 slice_sum4(const float *__restrict__ p, int64_t plane, int slices) {
+    float4 acc = *(const float4 *)p;
+    for (int z = 1; z < slices; ++z) {
+        const float4 a = *(const float4 *)(p + z * plane);
+        acc.x += a.x, acc.y += a.y, acc.z += a.z, acc.w += a.w;
+    }
+    return acc;
+}
+
+__device__ __forceinline__ float silu_mul(float g, float up) {
+    const double gd = (double)g;
+    return __fmul_rn((float)(gd / (1.0 + exp(-gd))), up);
+}
+
+// Split-K reduction fused with SwiGLU: W's rows are [gate; up] (hidden = rows
+// / 2); thread -> row m, gate/up columns u..u+3.  Each column is the
+// in-order slice sum (or the FP64 result for wide rows), then
+// h = f32(g/(1+exp(-g))) * up as swiglu_kernel computes it.
+__global__ __launch_bounds__(256) void gemm_reduce_swiglu4_kernel(const GemmArgs G, const float *__restrict__ partial,
+                                                                  const int32_t *__restrict__ wflags,
+                                                                  const int slices) {
+    const int64_t hidden = G.rows / 2;
+    const int64_t m = blockIdx.y, u = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+    int wide = 0;
+    for (int z = 0; z < slices; ++z) wide |= wflags[(int64_t)z * G.n + m];
+    if (u >= hidden) return;
+    float4 g, up;
+    if (wide) {
+        g = make_float4(wide_output(G, m, u), wide_output(G, m, u + 1), wide_output(G, m, u + 2),
+                        wide_output(G, m, u + 3));
+        up = make_float4(wide_output(G, m, hidden + u), wide_output(G, m, hidden + u + 1),
+                         wide_output(G, m, hidden + u + 2), wide_output(G, m, hidden + u + 3));
+    } else {
+        const int64_t plane = (int64_t)G.n * G.rows;
+        g = slice_sum4(partial + m * G.rows + u, plane, slices);
+        up = slice_sum4(partial + m * G.rows + hidden + u, plane, slices);
+    }
+    const float4 h = make_float4(silu_mul(g.x, up.x), silu_mul(g.y, up.y), silu_mul(g.z, up.z), silu_mul(g.w, up.w));
+    *(float4 *)(G.swiglu_out + m * hidden + u) = h;
+}
+
 struct GemmPlan {
     bool x3;  // bf16 MFMA kernel (Q8 / Q4, cols % 64 == 0)
     int bm, slices, kper;
@@ -734,11 +776,22 @@ int launch_gemm(hipStream_t s, const GemmArgs &a, void *scratch, size_t scratch_
         partial = (float *)scratch;
         wflags = (int32_t *)(partial + (size_t)p.slices * a.n * a.rows);
     }
+    if (a.swiglu_out && (a.residual || a.rows % 8 || ((uintptr_t)a.swiglu_out & 15)))
+        return fail(SRQ_EINVAL, "gemm: SwiGLU output needs an even row split, 16-byte alignment and no residual");
     if (p.bm == 32)
         launch_fmt<32>(s, a, p, partial, wflags);
     else
         launch_fmt<64>(s, a, p, partial, wflags);
     SRQ_HIP(hipGetLastError());
+    if (a.swiglu_out) {
+        if (p.slices > 1) {
+            dim3 grid((unsigned)((a.rows / 8 + 255) / 256), (unsigned)a.n);
+            gemm_reduce_swiglu4_kernel<<<grid, 256, 0, s>>>(a, partial, wflags, p.slices);
+            SRQ_HIP(hipGetLastError());
+            return SRQ_OK;
+        }
+        return launch_swiglu(s, a.y, a.n, (int32_t)(a.rows / 2), a.swiglu_out);
+    }
     if (p.slices > 1) {
         const bool vec4 = a.rows % 4 == 0 && a.y_stride % 4 == 0 && ((uintptr_t)a.y & 15) == 0 &&
                           (!a.residual || ((uintptr_t)a.residual & 15) == 0);

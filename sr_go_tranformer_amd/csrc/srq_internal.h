@@ -116,6 +116,10 @@ struct GemmArgs {
     float *y;           // [n x y_stride]
     int64_t y_stride;
     const float *residual;  // y = residual + acc when non-null (may alias y)
+    // SwiGLU output (nullable): W's rows are [gate (rows/2); up (rows/2)] and
+    // swiglu_out[m][u] = f32(g/(1+exp(-g))) * up (M:6411-6413), stride
+    // rows/2; y is then only a temporary (written when K is not split).
+    float *swiglu_out;
 };
 // y = x . W^T (+ residual) on MFMA.  Rows holding a wide |x| are computed
 // in FP64.  scratch: gemm_scratch_bytes(fmt, n, rows, cols) bytes of device
