@@ -980,9 +980,15 @@ int enqueue_layers(srq_exec *e, Workspace &ws, srq_model *m, srq_pool *pool, int
                 SRQ_CHECK(launch_gemv(e->stream, a));
             }
         } else {
-            SRQ_CHECK(launch_rmsnorm(e->stream, X, L.n1, N, n, (int32_t)d, c.norm_eps));
-            SRQ_CHECK(run_linear(e, ws, L.qkv, N, n, W2, d + 2 * kd, nullptr, 0.0, nullptr, kStepGemmRows));
-            SRQ_CHECK(launch_rope_kv(e->stream, W2, L.bias, n, (int32_t)d, (int32_t)kd, m->hd, m->cos_t, m->sin_t, Q, meta));
+            // N holds RMSNorm(X, n1) already when the previous layer's down
+            // projection wrote it from its reduction.
+            if (l == 0) SRQ_CHECK(launch_rmsnorm(e->stream, X, L.n1, N, n, (int32_t)d, c.norm_eps));
+            // q/k/v GEMM with bias, RoPE and the KV write in its reduction.
+            SRQ_CHECK(ensure(ws.flags, gemm_scratch_bytes(L.qkv.fmt, n, L.qkv.rows, L.qkv.cols), e->stream));
+            GemmArgs g{L.qkv.fmt, L.qkv.values, L.qkv.scales, L.qkv.rows, L.qkv.cols, N, n, W2, d + 2 * kd,
+                       nullptr, nullptr};
+            g.rope = GemmRope{Q, L.bias, (int32_t)d, (int32_t)kd, m->hd, m->cos_t, m->sin_t, meta};
+            SRQ_CHECK(launch_gemm(e->stream, g, ws.flags.p, ws.flags.n));
         }
         AttnArgs at{};
         at.q = Q;
@@ -997,7 +1003,17 @@ int enqueue_layers(srq_exec *e, Workspace &ws, srq_model *m, srq_pool *pool, int
         at.ntiles = dm.ntiles;
         SRQ_CHECK(launch_attention(e->stream, at, as<float>(ws.ATT), as<int32_t>(ws.ATTC)));
         // O projection + residual (M:6398-6400).
-        SRQ_CHECK(run_linear(e, ws, L.o, A, n, X, d, nullptr, 0.0, X, kStepGemmRows));
+        if (!use_gemm) {
+            SRQ_CHECK(run_linear(e, ws, L.o, A, n, X, d, nullptr, 0.0, X, kStepGemmRows));
+        } else {
+            // with RMSNorm(X, n2) -> N in its reduction
+            SRQ_CHECK(ensure(ws.flags, gemm_scratch_bytes(L.o.fmt, n, L.o.rows, L.o.cols), e->stream));
+            GemmArgs g{L.o.fmt, L.o.values, L.o.scales, L.o.rows, L.o.cols, A, n, X, d, X, nullptr};
+            g.norm_w = L.n2;
+            g.norm_eps = c.norm_eps;
+            g.norm_out = N;
+            SRQ_CHECK(launch_gemm(e->stream, g, ws.flags.p, ws.flags.n));
+        }
         if (!use_gemm) {
             for (int32_t r0 = 0; r0 < n; r0 += nbg) {
                 GemvArgs a{};
@@ -1017,7 +1033,6 @@ int enqueue_layers(srq_exec *e, Workspace &ws, srq_model *m, srq_pool *pool, int
                 SRQ_CHECK(launch_gemv(e->stream, a));
             }
         } else {
-            SRQ_CHECK(launch_rmsnorm(e->stream, X, L.n2, N, n, (int32_t)d, c.norm_eps));
             // gate/up GEMM with SwiGLU in its split-K reduction (W2 is only
             // a temporary when K is not split).
             SRQ_CHECK(ensure(ws.flags, gemm_scratch_bytes(L.gu.fmt, n, L.gu.rows, L.gu.cols), e->stream));
@@ -1025,7 +1040,17 @@ int enqueue_layers(srq_exec *e, Workspace &ws, srq_model *m, srq_pool *pool, int
             SRQ_CHECK(launch_gemm(e->stream, g, ws.flags.p, ws.flags.n));
         }
         // down + residual (M:6415-6417).
-        SRQ_CHECK(run_linear(e, ws, L.down, Hh, n, X, d, nullptr, 0.0, X, kStepGemmRows));
+        if (!use_gemm || l + 1 == c.layers) {
+            SRQ_CHECK(run_linear(e, ws, L.down, Hh, n, X, d, nullptr, 0.0, X, kStepGemmRows));
+        } else {
+            // with the next layer's RMSNorm(X, n1) -> N in its reduction
+            SRQ_CHECK(ensure(ws.flags, gemm_scratch_bytes(L.down.fmt, n, L.down.rows, L.down.cols), e->stream));
+            GemmArgs g{L.down.fmt, L.down.values, L.down.scales, L.down.rows, L.down.cols, Hh, n, X, d, X, nullptr};
+            g.norm_w = m->L[l + 1].n1;
+            g.norm_eps = c.norm_eps;
+            g.norm_out = N;
+            SRQ_CHECK(launch_gemm(e->stream, g, ws.flags.p, ws.flags.n));
+        }
     }
     return SRQ_OK;
 }

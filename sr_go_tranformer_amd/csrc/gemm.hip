@@ -280,6 +280,24 @@ __global__ __launch_bounds__(256) void gemm_kernel(const GemmArgs G, float *__re
     }
 }
 
+// Sum over the K slices z of p[z * plane], added in slice order.  The loads
+// go out eight slices at a time (a loop of one load per add would wait a
+// full memory latency per slice).
+template <typename V>
+__device__ __forceinline__ V slice_sum(const float *__restrict__ p, int64_t plane, int slices) {
+    V acc = *(const V *)p;
+    for (int z = 1; z < slices; z += 8) {
+        V a[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            if (z + i < slices) a[i] = *(const V *)(p + (int64_t)(z + i) * plane);
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            if (z + i < slices) acc += a[i];
+    }
+    return acc;
+}
+
 // y[m][j] = residual + sum over slices z (in order) of partial[z][m][j];
 // rows flagged wide by any slice take the FP64 path instead.
 __global__ __launch_bounds__(256) void gemm_reduce_kernel(const GemmArgs G, const float *__restrict__ partial,
@@ -292,10 +310,7 @@ __global__ __launch_bounds__(256) void gemm_reduce_kernel(const GemmArgs G, cons
     if (wide) {
         v = wide_output(G, m, j);
     } else {
-        const int64_t plane = (int64_t)G.n * G.rows;
-        const float *p = partial + m * G.rows + j;
-        float s = p[0];
-        for (int z = 1; z < slices; ++z) s += p[z * plane];
+        const float s = slice_sum<float>(partial + m * G.rows + j, (int64_t)G.n * G.rows, slices);
         v = G.residual ? G.residual[m * G.y_stride + j] + s : s;
     }
     G.y[m * G.y_stride + j] = v;
@@ -614,8 +629,7 @@ __global__ __launch_bounds__(256, 2) void gemm_x3_kernel(const GemmArgs G, float
 }
 
 // The same for four consecutive outputs (rows, y_stride and the plane are
-// multiples of 4): float4 loads, four slices in flight at a time, the sum
-// still taken in slice order.
+// multiples of 4): float4 loads, the sum still taken in slice order.
 __global__ __launch_bounds__(256) void gemm_reduce4_kernel(const GemmArgs G, const float *__restrict__ partial,
                                                            const int32_t *__restrict__ wflags, const int slices) {
     const int64_t m = blockIdx.y, j = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
@@ -627,23 +641,8 @@ __global__ __launch_bounds__(256) void gemm_reduce4_kernel(const GemmArgs G, con
         v = make_float4(wide_output(G, m, j), wide_output(G, m, j + 1), wide_output(G, m, j + 2),
                         wide_output(G, m, j + 3));
     } else {
-        const int64_t plane = (int64_t)G.n * G.rows;
-        const float *p = partial + m * G.rows + j;
-        float4 acc = *(const float4 *)p;
-        int z = 1;
-        for (; z + 4 <= slices; z += 4) {
-            const float4 a = *(const float4 *)(p + z * plane), b = *(const float4 *)(p + (z + 1) * plane);
-            const float4 c = *(const float4 *)(p + (z + 2) * plane), d = *(const float4 *)(p + (z + 3) * plane);
-            acc.x += a.x, acc.y += a.y, acc.z += a.z, acc.w += a.w;
-            acc.x += b.x, acc.y += b.y, acc.z += b.z, acc.w += b.w;
-            acc.x += c.x, acc.y += c.y, acc.z += c.z, acc.w += c.w;
-            acc.x += d.x, acc.y += d.y, acc.z += d.z, acc.w += d.w;
-        }
-        for (; z < slices; ++z) {
-            const float4 a = *(const float4 *)(p + z * plane);
-            acc.x += a.x, acc.y += a.y, acc.z += a.z, acc.w += a.w;
-        }
-        v = acc;
+        const floatx4 acc = slice_sum<floatx4>(partial + m * G.rows + j, (int64_t)G.n * G.rows, slices);
+        v = make_float4(acc.x, acc.y, acc.z, acc.w);
         if (G.residual) {
             const float4 r = *(const float4 *)(G.residual + m * G.y_stride + j);
             v = make_float4(r.x + acc.x, r.y + acc.y, r.z + acc.z, r.w + acc.w);
@@ -652,14 +651,9 @@ __global__ __launch_bounds__(256) void gemm_reduce4_kernel(const GemmArgs G, con
     *(float4 *)(G.y + m * G.y_stride + j) = v;
 }
 
-// Sum of column j's K slices for row m, in slice order (as gemm_reduce_kernel).
 __device__ __forceinline__ float4 slice_sum4(const float *__restrict__ p, int64_t plane, int slices) {
-    float4 acc = *(const float4 *)p;
-    for (int z = 1; z < slices; ++z) {
-        const float4 a = *(const float4 *)(p + z * plane);
-        acc.x += a.x, acc.y += a.y, acc.z += a.z, acc.w += a.w;
-    }
-    return acc;
+    const floatx4 a = slice_sum<floatx4>(p, plane, slices);
+    return make_float4(a.x, a.y, a.z, a.w);
 }
 
 __device__ __forceinline__ float silu_mul(float g, float up) {
@@ -692,6 +686,113 @@ __global__ __launch_bounds__(256) void gemm_reduce_swiglu4_kernel(const GemmArgs
     }
     const float4 h = make_float4(silu_mul(g.x, up.x), silu_mul(g.y, up.y), silu_mul(g.z, up.z), silu_mul(g.w, up.w));
     *(float4 *)(G.swiglu_out + m * hidden + u) = h;
+}
+
+constexpr int kNormThreads = 1024;
+constexpr int kNormVec = 2;  // float4 columns per thread of the norm reduction: rows <= 8192
+
+// Split-K reduction fused with the next RMSNorm: one workgroup per
+// activation row m.  y[m] is the in-order slice sum plus the residual (or
+// the FP64 result for wide rows), as gemm_reduce4_kernel writes it; then
+// norm_out[m] = (y*a)*w with a = f32(1/sqrt(Sum f64(y^2)/d + eps)) (rmsInto,
+// M:6182-6194) from the values still in registers.
+__global__ __launch_bounds__(kNormThreads) void gemm_reduce_norm4_kernel(const GemmArgs G,
+                                                                         const float *__restrict__ partial,
+                                                                         const int32_t *__restrict__ wflags,
+                                                                         const int slices) {
+    __shared__ double red[kNormThreads / 64];
+    const int64_t m = blockIdx.x;
+    const int tid = threadIdx.x;
+    int wide = 0;
+    for (int z = 0; z < slices; ++z) wide |= wflags[(int64_t)z * G.n + m];
+    const int64_t plane = (int64_t)G.n * G.rows;
+    float4 v[kNormVec];
+    double ss = 0.0;
+#pragma unroll
+    for (int k = 0; k < kNormVec; ++k) {
+        const int64_t j = ((int64_t)k * kNormThreads + tid) * 4;
+        if (j >= G.rows) break;
+        float4 t;
+        if (wide) {
+            t = make_float4(wide_output(G, m, j), wide_output(G, m, j + 1), wide_output(G, m, j + 2),
+                            wide_output(G, m, j + 3));
+        } else {
+            t = slice_sum4(partial + m * G.rows + j, plane, slices);
+            if (G.residual) {
+                const float4 r = *(const float4 *)(G.residual + m * G.y_stride + j);
+                t = make_float4(r.x + t.x, r.y + t.y, r.z + t.z, r.w + t.w);
+            }
+        }
+        *(float4 *)(G.y + m * G.y_stride + j) = t;
+        v[k] = t;
+        ss += (double)t.x * (double)t.x + (double)t.y * (double)t.y + (double)t.z * (double)t.z +
+              (double)t.w * (double)t.w;
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+    if ((tid & 63) == 0) red[tid >> 6] = ss;
+    __syncthreads();
+    double tot = 0.0;
+    for (int w = 0; w < kNormThreads / 64; ++w) tot += red[w];
+    const float a = (float)(1.0 / sqrt(tot / (double)G.rows + G.norm_eps));
+#pragma unroll
+    for (int k = 0; k < kNormVec; ++k) {
+        const int64_t j = ((int64_t)k * kNormThreads + tid) * 4;
+        if (j >= G.rows) break;
+        const float4 w = *(const float4 *)(G.norm_w + j);
+        const float4 t = v[k];
+        *(float4 *)(G.norm_out + m * G.rows + j) =
+            make_float4(__fmul_rn(__fmul_rn(t.x, a), w.x), __fmul_rn(__fmul_rn(t.y, a), w.y),
+                        __fmul_rn(__fmul_rn(t.z, a), w.z), __fmul_rn(__fmul_rn(t.w, a), w.w));
+    }
+}
+
+// Split-K reduction fused with RoPE and the KV write (the arithmetic of
+// rope_kv_kernel): thread t of row m takes RoPE pair t (j, j + head_dim/2) of
+// a q or k head, or past the pairs one v element.
+__global__ __launch_bounds__(256) void gemm_reduce_rope_kernel(const GemmArgs G, const float *__restrict__ partial,
+                                                               const int32_t *__restrict__ wflags, const int slices) {
+    const GemmRope &R = G.rope;
+    const int64_t m = blockIdx.y;
+    const int dim = R.dim, kvdim = R.kvdim, half = R.head_dim / 2, pairs = (dim + kvdim) / 2;
+    const int t = blockIdx.x * 256 + threadIdx.x;
+    int wide = 0;
+    for (int z = 0; z < slices; ++z) wide |= wflags[(int64_t)z * G.n + m];
+    if (t >= pairs + kvdim) return;
+    const int64_t plane = (int64_t)G.n * G.rows;
+    auto column = [&](int64_t j) {
+        return wide ? wide_output(G, m, j) : slice_sum<float>(partial + m * G.rows + j, plane, slices);
+    };
+    const RowMeta &meta = R.meta;
+    const int pos = meta.pos[m];
+    const int page = meta.pages[(int64_t)meta.sess[m] * meta.pt_stride + pos / kPageTokens];
+    float *kr = meta.kv_pool + (int64_t)page * meta.page_elems + (int64_t)meta.layer * 2 * kPageTokens * kvdim +
+                (int64_t)(pos % kPageTokens) * kvdim;
+    if (t < pairs) {
+        const int h = t / half, j = t - h * half;
+        const int i0 = h * R.head_dim + j, i1 = i0 + half;
+        float a = column(i0), z = column(i1);
+        if (R.bias) {
+            a = __fadd_rn(a, R.bias[i0]);
+            z = __fadd_rn(z, R.bias[i1]);
+        }
+        const float c = R.cos_t[(int64_t)pos * half + j], s = R.sin_t[(int64_t)pos * half + j];
+        // x' = a*c - z*s ; z' = a*s + z*c  (M:5283-5285), unfused
+        const float na = __fsub_rn(__fmul_rn(a, c), __fmul_rn(z, s));
+        const float nz = __fadd_rn(__fmul_rn(a, s), __fmul_rn(z, c));
+        if (i0 < dim) {
+            R.q[m * dim + i0] = na;
+            R.q[m * dim + i1] = nz;
+        } else {
+            kr[i0 - dim] = na;
+            kr[i1 - dim] = nz;
+        }
+    } else {
+        const int j = t - pairs;
+        float v = column(dim + kvdim + j);
+        if (R.bias) v = __fadd_rn(v, R.bias[dim + kvdim + j]);
+        kr[(int64_t)kPageTokens * kvdim + j] = v;
+    }
 }
 
 struct GemmPlan {
@@ -778,11 +879,44 @@ int launch_gemm(hipStream_t s, const GemmArgs &a, void *scratch, size_t scratch_
     }
     if (a.swiglu_out && (a.residual || a.rows % 8 || ((uintptr_t)a.swiglu_out & 15)))
         return fail(SRQ_EINVAL, "gemm: SwiGLU output needs an even row split, 16-byte alignment and no residual");
+    if (a.norm_out && (!a.norm_w || a.y_stride != a.rows || a.rows > (int64_t)INT32_MAX))
+        return fail(SRQ_EINVAL, "gemm: RMSNorm output needs a norm weight and y_stride == rows");
+    if (a.rope.q && (a.residual || a.swiglu_out || a.norm_out || a.rope.head_dim < 2 || a.rope.head_dim % 2 ||
+                     a.rope.dim % a.rope.head_dim || a.rope.kvdim % a.rope.head_dim ||
+                     a.rows != (int64_t)a.rope.dim + 2 * (int64_t)a.rope.kvdim || a.y_stride != a.rows))
+        return fail(SRQ_EINVAL, "gemm: RoPE/KV output needs rows = dim + 2*kvdim in whole heads and no other epilogue");
     if (p.bm == 32)
         launch_fmt<32>(s, a, p, partial, wflags);
     else
         launch_fmt<64>(s, a, p, partial, wflags);
     SRQ_HIP(hipGetLastError());
+    if (a.rope.q) {
+        if (p.slices > 1) {
+            const int work = (a.rope.dim + a.rope.kvdim) / 2 + a.rope.kvdim;
+            dim3 grid((unsigned)((work + 255) / 256), (unsigned)a.n);
+            gemm_reduce_rope_kernel<<<grid, 256, 0, s>>>(a, partial, wflags, p.slices);
+            SRQ_HIP(hipGetLastError());
+            return SRQ_OK;
+        }
+        return launch_rope_kv(s, a.y, a.rope.bias, a.n, a.rope.dim, a.rope.kvdim, a.rope.head_dim, a.rope.cos_t,
+                              a.rope.sin_t, a.rope.q, a.rope.meta);
+    }
+    if (a.norm_out) {
+        const bool fused = p.slices > 1 && a.rows % 4 == 0 && a.rows <= 4 * kNormThreads * kNormVec &&
+                           ((((uintptr_t)a.y) | ((uintptr_t)a.norm_w) | ((uintptr_t)a.norm_out) |
+                             (a.residual ? (uintptr_t)a.residual : 0)) & 15) == 0;
+        if (fused) {
+            gemm_reduce_norm4_kernel<<<(unsigned)a.n, kNormThreads, 0, s>>>(a, partial, wflags, p.slices);
+            SRQ_HIP(hipGetLastError());
+            return SRQ_OK;
+        }
+        if (p.slices > 1) {
+            dim3 grid((unsigned)((a.rows + 255) / 256), (unsigned)a.n);
+            gemm_reduce_kernel<<<grid, 256, 0, s>>>(a, partial, wflags, p.slices);
+            SRQ_HIP(hipGetLastError());
+        }
+        return launch_rmsnorm(s, a.y, a.norm_w, a.norm_out, a.n, (int32_t)a.rows, a.norm_eps);
+    }
     if (a.swiglu_out) {
         if (p.slices > 1) {
             dim3 grid((unsigned)((a.rows / 8 + 255) / 256), (unsigned)a.n);

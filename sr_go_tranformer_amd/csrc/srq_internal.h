@@ -106,6 +106,17 @@ int gemv_max_rows(int fmt, int64_t cols, bool norm, int64_t extra_floats);
 int gemv_prepare();
 
 // ------------------------------------------------------------------ GEMM
+// RoPE/KV output of a q/k/v GEMM: W's rows are [q: dim | k: kvdim | v: kvdim]
+// (bias added first, then the half-split RoPE of M:5264-5289 on q and k); q
+// goes to q (stride dim), k and v into the rows' KV pages (M:6393-6395).
+struct GemmRope {
+    float *q;               // null: no RoPE/KV output
+    const float *bias;      // [dim + 2*kvdim] or null
+    int32_t dim, kvdim, head_dim;
+    const float *cos_t, *sin_t;  // [context x head_dim/2]
+    RowMeta meta;
+};
+
 struct GemmArgs {
     int fmt;
     const void *values;
@@ -120,6 +131,13 @@ struct GemmArgs {
     // swiglu_out[m][u] = f32(g/(1+exp(-g))) * up (M:6411-6413), stride
     // rows/2; y is then only a temporary (written when K is not split).
     float *swiglu_out;
+    // RMSNorm output (nullable): norm_out[m] = rmsInto(y[m], norm_w, eps)
+    // (M:6182-6194), the next matrix's input, stride rows; needs y_stride ==
+    // rows.  y is still written.
+    const float *norm_w;
+    double norm_eps;
+    float *norm_out;
+    GemmRope rope;  // rope.q non-null: RoPE/KV output; y is then only a temporary
 };
 // y = x . W^T (+ residual) on MFMA.  Rows holding a wide |x| are computed
 // in FP64.  scratch: gemm_scratch_bytes(fmt, n, rows, cols) bytes of device
