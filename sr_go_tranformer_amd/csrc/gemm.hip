@@ -298,13 +298,22 @@ __device__ __forceinline__ V slice_sum(const float *__restrict__ p, int64_t plan
     return acc;
 }
 
+// Whether any K slice flagged row m wide.  Each thread reads a share of the
+// flags, so the workgroup pays one memory latency (a loop over the slices in
+// every thread would pay one per slice).  Every thread of the workgroup
+// calls it.
+__device__ __forceinline__ int any_wide(const int32_t *__restrict__ wflags, int64_t n, int64_t m, int slices) {
+    int f = 0;
+    for (int z = threadIdx.x; z < slices; z += blockDim.x) f |= wflags[(int64_t)z * n + m];
+    return __syncthreads_or(f);
+}
+
 // y[m][j] = residual + sum over slices z (in order) of partial[z][m][j];
 // rows flagged wide by any slice take the FP64 path instead.
 __global__ __launch_bounds__(256) void gemm_reduce_kernel(const GemmArgs G, const float *__restrict__ partial,
                                                           const int32_t *__restrict__ wflags, const int slices) {
     const int64_t m = blockIdx.y, j = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    int wide = 0;
-    for (int z = 0; z < slices; ++z) wide |= wflags[(int64_t)z * G.n + m];
+    const int wide = any_wide(wflags, G.n, m, slices);
     if (j >= G.rows) return;
     float v;
     if (wide) {
@@ -633,8 +642,7 @@ __global__ __launch_bounds__(256, 2) void gemm_x3_kernel(const GemmArgs G, float
 __global__ __launch_bounds__(256) void gemm_reduce4_kernel(const GemmArgs G, const float *__restrict__ partial,
                                                            const int32_t *__restrict__ wflags, const int slices) {
     const int64_t m = blockIdx.y, j = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
-    int wide = 0;
-    for (int z = 0; z < slices; ++z) wide |= wflags[(int64_t)z * G.n + m];
+    const int wide = any_wide(wflags, G.n, m, slices);
     if (j >= G.rows) return;
     float4 v;
     if (wide) {
@@ -670,8 +678,7 @@ __global__ __launch_bounds__(256) void gemm_reduce_swiglu4_kernel(const GemmArgs
                                                                   const int slices) {
     const int64_t hidden = G.rows / 2;
     const int64_t m = blockIdx.y, u = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
-    int wide = 0;
-    for (int z = 0; z < slices; ++z) wide |= wflags[(int64_t)z * G.n + m];
+    const int wide = any_wide(wflags, G.n, m, slices);
     if (u >= hidden) return;
     float4 g, up;
     if (wide) {
@@ -703,8 +710,7 @@ __global__ __launch_bounds__(kNormThreads) void gemm_reduce_norm4_kernel(const G
     __shared__ double red[kNormThreads / 64];
     const int64_t m = blockIdx.x;
     const int tid = threadIdx.x;
-    int wide = 0;
-    for (int z = 0; z < slices; ++z) wide |= wflags[(int64_t)z * G.n + m];
+    const int wide = any_wide(wflags, G.n, m, slices);
     const int64_t plane = (int64_t)G.n * G.rows;
     float4 v[kNormVec];
     double ss = 0.0;
@@ -756,8 +762,7 @@ __global__ __launch_bounds__(256) void gemm_reduce_rope_kernel(const GemmArgs G,
     const int64_t m = blockIdx.y;
     const int dim = R.dim, kvdim = R.kvdim, half = R.head_dim / 2, pairs = (dim + kvdim) / 2;
     const int t = blockIdx.x * 256 + threadIdx.x;
-    int wide = 0;
-    for (int z = 0; z < slices; ++z) wide |= wflags[(int64_t)z * G.n + m];
+    const int wide = any_wide(wflags, G.n, m, slices);
     if (t >= pairs + kvdim) return;
     const int64_t plane = (int64_t)G.n * G.rows;
     auto column = [&](int64_t j) {
