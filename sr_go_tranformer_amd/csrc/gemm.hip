@@ -341,8 +341,8 @@ __global__ __launch_bounds__(256) void gemm_reduce_kernel(const GemmArgs G, cons
 // running sum: acc = fma(block, scale, acc) (the per-block form of
 // linearQ8Into's dequantised dot, M:3942-4000).
 //
-// Tiling: 4 waves, each owning TM x 4 tiles of 16x16 (TM*16 activation rows
-// x 64 features); a workgroup covers TM*16 rows x 256 features.
+// Tiling: 4 waves, each owning TM x TN tiles of 16x16 (TM*16 activation rows
+// x TN*16 features); a workgroup covers TM*16 rows x 64*TN features.
 //  - Weights go from HBM straight into MFMA operand registers: lane
 //    (i = lane%16, q = lane/16) of feature tile tn loads the 16 codes
 //    [16q, 16q+16) of its row's block (Q8: 16 bytes, Q4: 8 bytes); the
@@ -354,7 +354,7 @@ __global__ __launch_bounds__(256) void gemm_reduce_kernel(const GemmArgs G, cons
 //    the same K map as the weights.
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
-constexpr int XBN = 256, XLD = 72;
+constexpr int XLD = 72;
 
 template <int TM>
 struct XTile {
@@ -489,10 +489,10 @@ __device__ __forceinline__ float xstore_a(__bf16 *As, int tid, const float4 (&a)
 // in flight.  Rows past the ends are clamped (weights: scale 0; activations:
 // row n-1, whose outputs are never stored) so the block body has no
 // per-lane branches.
-template <int FMT, int TM>
+template <int FMT, int TM, int TN>
 __global__ __launch_bounds__(256, 2) void gemm_x3_kernel(const GemmArgs G, float *__restrict__ partial,
                                                                        int32_t *__restrict__ wflags, const int kper) {
-    constexpr int BM = XTile<TM>::BM, NV = XTile<TM>::NV, PLANE = XTile<TM>::PLANE, TN = 4;
+    constexpr int BM = XTile<TM>::BM, NV = XTile<TM>::NV, PLANE = XTile<TM>::PLANE, XBN = 64 * TN;
     constexpr int FPT = XTile<TM>::FPT, TPR = XTile<TM>::TPR;
     constexpr int64_t BB = FMT == SRQ_Q8 ? kBlock : kBlock / 2;  // weight bytes per row and block
     typedef typename XRaw<FMT>::type R;
@@ -500,7 +500,7 @@ __global__ __launch_bounds__(256, 2) void gemm_x3_kernel(const GemmArgs G, float
     __shared__ int row_wide[BM];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int li = lane & 15, q = lane >> 4;
-    const int64_t n0 = (int64_t)blockIdx.x * XBN + wave * 64, m0 = (int64_t)blockIdx.y * BM;
+    const int64_t n0 = (int64_t)blockIdx.x * XBN + wave * 16 * TN, m0 = (int64_t)blockIdx.y * BM;
     const int64_t cols = G.cols, groups = cols / kBlock;
     const int gbeg = (int)blockIdx.z * kper;
     const int gend = min(gbeg + kper, (int)groups), glast = gend - 1;
@@ -633,7 +633,7 @@ __global__ __launch_bounds__(256, 2) void gemm_x3_kernel(const GemmArgs G, float
     for (int mi = 0; mi < BM; ++mi) {
         if (!row_wide[mi] || m0 + mi >= G.n) continue;
         const int64_t j = (int64_t)blockIdx.x * XBN + tid;
-        if (j < G.rows) G.y[(m0 + mi) * G.y_stride + j] = wide_output(G, m0 + mi, j);
+        if (tid < XBN && j < G.rows) G.y[(m0 + mi) * G.y_stride + j] = wide_output(G, m0 + mi, j);
     }
 }
 
@@ -802,7 +802,7 @@ __global__ __launch_bounds__(256) void gemm_reduce_rope_kernel(const GemmArgs G,
 
 struct GemmPlan {
     bool x3;  // bf16 MFMA kernel (Q8 / Q4, cols % 64 == 0)
-    int bm, slices, kper;
+    int bm, tn, slices, kper;  // tn: 16-feature tiles per wave of the bf16 kernel
 };
 
 // Tile height from n.  With fewer tiles than CUs, K slices bring the grid
@@ -813,7 +813,13 @@ GemmPlan plan_gemm(int fmt, int32_t n, int64_t rows, int64_t cols) {
     GemmPlan p;
     p.x3 = (fmt == SRQ_Q8 || fmt == SRQ_Q4) && cols % kBlock == 0;
     p.bm = n <= 32 ? 32 : 64;
-    const int bn = p.x3 ? XBN : BN, bk = p.x3 ? kBlock : BK;
+    // 128-feature tiles for 32-row tiles of narrow outputs: twice the
+    // tiles, so fewer K slices and half the partial-sum traffic per weight
+    // byte (Llama-3.2-3B shapes at 24-32 rows: 3072 x 3072 17.2 -> 13.5 us,
+    // 3072 x 8192 24.9 -> 23.3 us, 5120 x 3072 20.0 -> 18.9 us; at 16384
+    // rows the 256-feature tile stays ahead, 30.4 against 33.5 us).
+    p.tn = p.bm == 32 && rows <= 8192 ? 2 : 4;
+    const int bn = p.x3 ? 64 * p.tn : BN, bk = p.x3 ? kBlock : BK;
     const int64_t tiles = ((rows + bn - 1) / bn) * ((n + p.bm - 1) / p.bm);
     const int ksteps = (int)(cols / bk), min_steps = kMinSliceInputs / bk;
     int slices = 1;
@@ -837,8 +843,12 @@ void launch_tiles(hipStream_t s, const GemmArgs &a, const GemmPlan &p, float *pa
         gemm_kernel<FMT, BMT><<<grid, 256, 0, s>>>(a, partial, wflags, p.kper);
     } else {
         if (p.x3) {
-            dim3 grid((unsigned)((a.rows + XBN - 1) / XBN), (unsigned)((a.n + BMT - 1) / BMT), (unsigned)p.slices);
-            gemm_x3_kernel<FMT, BMT / 16><<<grid, 256, 0, s>>>(a, partial, wflags, p.kper);
+            const int xbn = 64 * p.tn;
+            dim3 grid((unsigned)((a.rows + xbn - 1) / xbn), (unsigned)((a.n + BMT - 1) / BMT), (unsigned)p.slices);
+            if (p.tn == 2)
+                gemm_x3_kernel<FMT, BMT / 16, 2><<<grid, 256, 0, s>>>(a, partial, wflags, p.kper);
+            else
+                gemm_x3_kernel<FMT, BMT / 16, 4><<<grid, 256, 0, s>>>(a, partial, wflags, p.kper);
         } else {
             dim3 grid((unsigned)((a.rows + BN - 1) / BN), (unsigned)((a.n + BMT - 1) / BMT), (unsigned)p.slices);
             gemm_kernel<FMT, BMT><<<grid, 256, 0, s>>>(a, partial, wflags, p.kper);
