@@ -20,6 +20,15 @@
 // independent of the order threads add in: results are deterministic.  The
 // reference sums f64 probabilities in sorted order; the two agree except
 // when a cut falls within ~1e-12 of a candidate boundary.
+//
+// Passes over the row: one for the range and the first maximum, one for the
+// masses and the first-level histogram of every candidate, then one per cut
+// that gathers its bucket (more only when a bucket holds over 2048
+// candidates).  The first-level histogram serves all three cuts: every cut
+// is a prefix of the candidate order whose target lies within the prefix
+// kept so far, so the buckets before the one holding it are kept whole and
+// the unfiltered histogram finds the same bucket.  A candidate's mass is
+// recomputed where it is needed (it is a pure function of its value).
 #include <cfloat>
 #include <climits>
 
@@ -48,6 +57,8 @@ __device__ __forceinline__ bool before(double va, int ia, double vb, int ib) {
 struct SampleLds {
     uint32_t hcount[kBuckets];
     unsigned long long hmass[kBuckets];
+    uint32_t h0count[kBuckets];           // first-level histogram over [vmin, vmax]
+    unsigned long long h0mass[kBuckets];
     double lv[kList];
     int li[kList];
     unsigned long long lp[kList];
@@ -141,13 +152,12 @@ __device__ __forceinline__ int block_min_int(int v, SampleLds &s) {
     return r;
 }
 
-__global__ __launch_bounds__(kST) void sample_kernel(const SampleArgs A, unsigned long long *__restrict__ pscr) {
+__global__ __launch_bounds__(kST) void sample_kernel(const SampleArgs A) {
     extern __shared__ uint32_t seen[];  // history bitmap, (vocab + 31) / 32 words
     __shared__ SampleLds s;
     const int row = blockIdx.x, tid = threadIdx.x;
     const int vocab = A.vocab;
     const float *lg = A.logits + (int64_t)(A.row_ids ? A.row_ids[row] : row) * vocab;
-    unsigned long long *P = pscr + (int64_t)row * vocab;
     const int blocked = A.blocked ? A.blocked[row] : -1;
     const double T = A.temperature, rp = A.repeat_penalty;
     const bool use_seen = T != 0.0 || rp != 1.0;
@@ -211,6 +221,10 @@ __global__ __launch_bounds__(kST) void sample_kernel(const SampleArgs A, unsigne
         return;
     }
 
+    // Integer mass of a candidate of value v: p = exp((v - vmax) / T) scaled
+    // by 2^44 and rounded.
+    auto mass_of = [&](double v) { return (unsigned long long)(exp((v - vmax) / T) * kFix + 0.5); };
+
     // Candidates precede the bounds kcut (top_k) and pcut (top_p) in order.
     Cand kcut{-DBL_MAX, INT_MAX}, pcut{-DBL_MAX, INT_MAX};
     auto member = [&](int i, double v) {
@@ -229,34 +243,38 @@ __global__ __launch_bounds__(kST) void sample_kernel(const SampleArgs A, unsigne
             const double scale = hi > lo ? (double)kBuckets / (hi - lo) : 0.0;
             los[level] = lo;
             scales[level] = scale;
-            for (int b = tid; b < kBuckets; b += kST) s.hcount[b] = 0, s.hmass[b] = 0;
-            __syncthreads();
             auto inside = [&](double v) {  // in the chosen bucket of every earlier level
                 for (int l = 0; l < level; ++l)
                     if (bucket_of(v, los[l], scales[l]) != chosen[l]) return false;
                 return true;
             };
-            for (int base = 0; base < vocab; base += kST * U) {
-                float x[U];
-                unsigned long long pm[U];
+            if (level == 0) {
+                // the first-level histogram of every candidate (pass B)
+                for (int b = tid; b < kBuckets; b += kST) s.hcount[b] = s.h0count[b], s.hmass[b] = s.h0mass[b];
+                __syncthreads();
+            } else {
+                for (int b = tid; b < kBuckets; b += kST) s.hcount[b] = 0, s.hmass[b] = 0;
+                __syncthreads();
+                for (int base = 0; base < vocab; base += kST * U) {
+                    float x[U];
 #pragma unroll
-                for (int u = 0; u < U; ++u) {
-                    const int i = base + u * kST + tid;
-                    x[u] = i < vocab ? lg[i] : 0.0f;
-                    pm[u] = i < vocab ? P[i] : 0ull;
-                }
+                    for (int u = 0; u < U; ++u) {
+                        const int i = base + u * kST + tid;
+                        x[u] = i < vocab ? lg[i] : 0.0f;
+                    }
 #pragma unroll
-                for (int u = 0; u < U; ++u) {
-                    const int i = base + u * kST + tid;
-                    if (i >= vocab) continue;
-                    const double v = value(i, x[u]);
-                    if (!member(i, v) || !inside(v)) continue;
-                    const int b = bucket_of(v, lo, scale);
-                    atomicAdd(&s.hcount[b], 1u);
-                    atomicAdd(&s.hmass[b], pm[u]);
+                    for (int u = 0; u < U; ++u) {
+                        const int i = base + u * kST + tid;
+                        if (i >= vocab) continue;
+                        const double v = value(i, x[u]);
+                        if (!member(i, v) || !inside(v)) continue;
+                        const int b = bucket_of(v, lo, scale);
+                        atomicAdd(&s.hcount[b], 1u);
+                        atomicAdd(&s.hmass[b], mass_of(v));
+                    }
                 }
+                __syncthreads();
             }
-            __syncthreads();
             // Running totals over buckets in descending order (bucket 2047
             // first): thread t owns buckets 2047-2t and 2046-2t.
             {
@@ -313,7 +331,7 @@ __global__ __launch_bounds__(kST) void sample_kernel(const SampleArgs A, unsigne
                 for (int i = tid; i < vocab; i += kST) {
                     const double v = value(i, lg[i]);
                     if (!member(i, v) || !inside(v) || bucket_of(v, lo, scale) != b) continue;
-                    bmn = fmin(bmn, v), bmx = fmax(bmx, v), pe = P[i];
+                    bmn = fmin(bmn, v), bmx = fmax(bmx, v), pe = mass_of(v);
                 }
                 bmn = block_min(bmn, s);
                 bmx = block_max(bmx, s);
@@ -390,12 +408,10 @@ __global__ __launch_bounds__(kST) void sample_kernel(const SampleArgs A, unsigne
             __syncthreads();
             for (int base = 0; base < vocab; base += kST * U) {
                 float x[U];
-                unsigned long long pm[U];
 #pragma unroll
                 for (int u = 0; u < U; ++u) {
                     const int i = base + u * kST + tid;
                     x[u] = i < vocab ? lg[i] : 0.0f;
-                    pm[u] = i < vocab ? P[i] : 0ull;
                 }
 #pragma unroll
                 for (int u = 0; u < U; ++u) {
@@ -404,7 +420,7 @@ __global__ __launch_bounds__(kST) void sample_kernel(const SampleArgs A, unsigne
                     const double v = value(i, x[u]);
                     if (!member(i, v) || !inside(v) || bucket_of(v, lo, scale) != b) continue;
                     const int k = atomicAdd(&s.list_n, 1);
-                    s.lv[k] = v, s.li[k] = i, s.lp[k] = pm[u];
+                    s.lv[k] = v, s.li[k] = i, s.lp[k] = mass_of(v);
                 }
             }
             __syncthreads();
@@ -462,7 +478,11 @@ __global__ __launch_bounds__(kST) void sample_kernel(const SampleArgs A, unsigne
         }
     };
 
-    // ---- pass B: integer masses and the total --------------------------------
+    // ---- pass B: integer masses, the total and the first-level histogram -----
+    // (buckets over [vmin, vmax], as locate's first level computes them)
+    for (int b = tid; b < kBuckets; b += kST) s.h0count[b] = 0, s.h0mass[b] = 0;
+    __syncthreads();
+    const double scale0 = vmax > vmin ? (double)kBuckets / (vmax - vmin) : 0.0;
     unsigned long long total = 0;
     for (int base = 0; base < vocab; base += kST * U) {
         float x[U];
@@ -474,14 +494,13 @@ __global__ __launch_bounds__(kST) void sample_kernel(const SampleArgs A, unsigne
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const int i = base + u * kST + tid;
-            if (i >= vocab) continue;
-            unsigned long long m = 0;
-            if (i != blocked) {
-                const double p = exp((value(i, x[u]) - vmax) / T);
-                m = (unsigned long long)(p * kFix + 0.5);
-            }
-            P[i] = m;
+            if (i >= vocab || i == blocked) continue;
+            const double v = value(i, x[u]);
+            const unsigned long long m = mass_of(v);
             total += m;
+            const int b = bucket_of(v, vmin, scale0);
+            atomicAdd(&s.h0count[b], 1u);
+            atomicAdd(&s.h0mass[b], m);
         }
     }
     total = block_sum(total, s);
@@ -496,8 +515,10 @@ __global__ __launch_bounds__(kST) void sample_kernel(const SampleArgs A, unsigne
         kcut = s.cut;
         // mass of the kept candidates
         unsigned long long m = 0;
-        for (int i = tid; i < vocab; i += kST)
-            if (member(i, value(i, lg[i]))) m += P[i];
+        for (int i = tid; i < vocab; i += kST) {
+            const double v = value(i, lg[i]);
+            if (member(i, v)) m += mass_of(v);
+        }
         total = block_sum(m, s);
     }
     // top_p: the shortest prefix with mass >= top_p * total (M:7398-7409).
@@ -539,13 +560,11 @@ __global__ __launch_bounds__(kST) void sample_kernel(const SampleArgs A, unsigne
 
 }  // namespace
 
-size_t sample_scratch_bytes(int32_t rows, int32_t vocab) { return (size_t)rows * vocab * 8; }
-
-int launch_sample(hipStream_t s, const SampleArgs &a, void *scratch) {
+int launch_sample(hipStream_t s, const SampleArgs &a) {
     if (a.rows <= 0) return SRQ_OK;
     const size_t lds = (size_t)((a.vocab + 31) / 32) * 4;
     if (lds > 48 * 1024) return fail(SRQ_EINVAL, "sample: vocabulary of %d ids exceeds the history bitmap", a.vocab);
-    sample_kernel<<<a.rows, kST, lds, s>>>(a, (unsigned long long *)scratch);
+    sample_kernel<<<a.rows, kST, lds, s>>>(a);
     SRQ_HIP(hipGetLastError());
     return SRQ_OK;
 }

@@ -177,8 +177,7 @@ struct SampleArgs {
     int32_t *ids;                // [rows] out
     int32_t *err;                // |= 1 non-finite logit, 2 no candidate, 4/8 selection limits
 };
-int launch_sample(hipStream_t s, const SampleArgs &a, void *scratch);
-size_t sample_scratch_bytes(int32_t rows, int32_t vocab);
+int launch_sample(hipStream_t s, const SampleArgs &a);
 
 // ------------------------------------------------------------- attention
 struct AttnArgs {
