@@ -360,20 +360,44 @@ __device__ __forceinline__ void merge_wave(const AttnArgs &A, const float *part,
 //   out_j = sum_i f32(exp(m_i - lse)) * o_i[j], FMA in split order.
 // One wave per head forms M and l (lanes stride the splits, then a
 // butterfly); the (head, dim) pairs spread over the threads, each pair
-// loading kMergeBatch splits at a time.
+// keeping two batches of kMergeBatch splits in flight.  Up to 256 splits a
+// lane loads all its {m, l} in one round.
 __device__ __forceinline__ void merge_splits(const AttnArgs &A, const float *part, int nsplit, int row, int h0,
                                              int nh, int hd, int used, float (*cf)[kMergeChunk], double *lse) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     for (int g = wave; g < nh; g += 4) {
         const int h = h0 + g;
         float M = -FLT_MAX;
-        for (int i = lane; i < used; i += 64) M = fmaxf(M, partial((float *)part, row, h, i, A.heads, nsplit, hd)[0]);
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
         double l = 0.0;
-        for (int i = lane; i < used; i += 64) {
-            const float *p = partial((float *)part, row, h, i, A.heads, nsplit, hd);
-            l += *(const double *)(p + 2) * exp((double)p[0] - (double)M);
+        if (used <= 256) {
+            float mv[4];
+            double lv[4];
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                const int i = lane + 64 * b;
+                mv[b] = -FLT_MAX;
+                lv[b] = 0.0;
+                if (i < used) {
+                    const float *p = partial((float *)part, row, h, i, A.heads, nsplit, hd);
+                    mv[b] = p[0];
+                    lv[b] = *(const double *)(p + 2);
+                }
+            }
+#pragma unroll
+            for (int b = 0; b < 4; ++b) M = fmaxf(M, mv[b]);
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
+#pragma unroll
+            for (int b = 0; b < 4; ++b)
+                if (lane + 64 * b < used) l += lv[b] * exp((double)mv[b] - (double)M);
+        } else {
+            for (int i = lane; i < used; i += 64) M = fmaxf(M, partial((float *)part, row, h, i, A.heads, nsplit, hd)[0]);
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
+            for (int i = lane; i < used; i += 64) {
+                const float *p = partial((float *)part, row, h, i, A.heads, nsplit, hd);
+                l += *(const double *)(p + 2) * exp((double)p[0] - (double)M);
+            }
         }
 #pragma unroll
         for (int o = 32; o > 0; o >>= 1) l += __shfl_xor(l, o, 64);
@@ -396,13 +420,29 @@ __device__ __forceinline__ void merge_splits(const AttnArgs &A, const float *par
             if (pidx >= nh * hd) break;
             const int g = pidx / hd, j = pidx - g * hd;
             const float *pb = partial((float *)part, row, h0 + g, c0, A.heads, nsplit, hd) + 4 + j;
-            for (int i0 = 0; i0 < cnt; i0 += kMergeBatch) {
-                float v[kMergeBatch];
+            // Two batches in flight: the next batch loads while this one's
+            // FMAs (in split order) run.
+            float va[kMergeBatch], vb[kMergeBatch];
 #pragma unroll
-                for (int b = 0; b < kMergeBatch; ++b) v[b] = pb[(int64_t)min(i0 + b, cnt - 1) * (hd + 4)];
+            for (int b = 0; b < kMergeBatch; ++b) va[b] = pb[(int64_t)min(b, cnt - 1) * (hd + 4)];
+            for (int i0 = 0; i0 < cnt; i0 += 2 * kMergeBatch) {
+                const int i1 = i0 + kMergeBatch;
+                if (i1 < cnt) {
+#pragma unroll
+                    for (int b = 0; b < kMergeBatch; ++b) vb[b] = pb[(int64_t)min(i1 + b, cnt - 1) * (hd + 4)];
+                }
 #pragma unroll
                 for (int b = 0; b < kMergeBatch; ++b)
-                    if (i0 + b < cnt) o[k] = __builtin_fmaf(cf[g][i0 + b], v[b], o[k]);
+                    if (i0 + b < cnt) o[k] = __builtin_fmaf(cf[g][i0 + b], va[b], o[k]);
+                if (i1 >= cnt) break;
+                if (i1 + kMergeBatch < cnt) {
+#pragma unroll
+                    for (int b = 0; b < kMergeBatch; ++b)
+                        va[b] = pb[(int64_t)min(i1 + kMergeBatch + b, cnt - 1) * (hd + 4)];
+                }
+#pragma unroll
+                for (int b = 0; b < kMergeBatch; ++b)
+                    if (i1 + b < cnt) o[k] = __builtin_fmaf(cf[g][i1 + b], vb[b], o[k]);
             }
         }
         __syncthreads();
