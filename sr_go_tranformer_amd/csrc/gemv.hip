@@ -747,8 +747,11 @@ __global__ __launch_bounds__(kStreamThreads) void gemv_stream_kernel(const GemvA
     const int U = unit_count<EPI>(A);
     // Units are dealt round-robin (u = wid + k*nwaves): at any moment the
     // waves together sweep one contiguous band of rows, which spreads the
-    // traffic over every HBM channel.
-    const int nwaves = (int)gridDim.x * kStreamWaves, wid = (int)blockIdx.x * kStreamWaves + wave;
+    // traffic over every HBM channel.  Waves are numbered wave-major
+    // (wid = wave * workgroups + workgroup), so when the units do not divide
+    // evenly the extra ones land on every CU alike (q/k/v: 3072 units on
+    // 2048 waves give each CU 12, not 16 on half of them and 8 on the rest).
+    const int nwaves = (int)gridDim.x * kStreamWaves, wid = wave * (int)gridDim.x + (int)blockIdx.x;
     const int myunits = wid < U ? (U - 1 - wid) / nwaves + 1 : 0;
     const int steps = myunits * nch;
     const int ulast = wid + (myunits - 1) * nwaves;
