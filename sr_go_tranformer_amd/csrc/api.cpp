@@ -892,6 +892,7 @@ struct StepMeta {
     int32_t pt_stride;
     int32_t *tiles = nullptr;  // query tiles {first row, rows} (AttnArgs::tiles)
     int32_t ntiles = 0;
+    bool plan_ready = false;   // the row plan in ws.PLAN is already current (decoder)
 };
 
 // Layout of the packed metadata buffer (device and pinned host mirror): at
@@ -941,8 +942,10 @@ int enqueue_layers(srq_exec *e, Workspace &ws, srq_model *m, srq_pool *pool, int
         // q/k/v epilogue (ws.PLAN is sized by ensure_workspace).
         kvoff = as<int64_t>(ws.PLAN);
         rope_cs = (float *)(kvoff + n);
-        RowMeta meta0 = make_meta(e, m, 0, dm.pt_stride, dm.pos, dm.sess, dm.pages, pool);
-        SRQ_CHECK(launch_row_plan(e->stream, meta0, n, (int32_t)kd, m->hd, m->cos_t, m->sin_t, kvoff, rope_cs));
+        if (!dm.plan_ready) {
+            RowMeta meta0 = make_meta(e, m, 0, dm.pt_stride, dm.pos, dm.sess, dm.pages, pool);
+            SRQ_CHECK(launch_row_plan(e->stream, meta0, n, (int32_t)kd, m->hd, m->cos_t, m->sin_t, kvoff, rope_cs));
+        }
     }
     // Batch rows per fused launch: q/k/v (norm, RoPE rows, bias) and gate/up (norm).
     const int nbq = gemv_max_rows(m->L[0].qkv.fmt, d, true, 8 * (int64_t)m->hd + (m->L[0].bias ? d + 2 * kd : 0));
@@ -1266,6 +1269,23 @@ extern "C" {
 
 int srq_decoder_destroy(srq_decoder *d);
 
+// The first step's input: the embedding row of the first token and the row
+// plan of its position.  Every step's tail then prepares the next one's.
+static int enqueue_decode_input(srq_decoder *d) {
+    srq_exec *e = d->e;
+    srq_model *m = d->m;
+    int32_t *pos = d->dbuf, *sess = d->dbuf + 1, *embed_id = d->dbuf + 3, *pt = d->dbuf + 6;
+    Workspace &ws = d->ws;
+    SRQ_CHECK(launch_dequant_rows(e->stream, m->embed.fmt, m->c.dim, m->embed.values, m->embed.scales, embed_id, 1,
+                                  as<float>(ws.X)));
+    int64_t *kvoff = as<int64_t>(ws.PLAN);
+    RowMeta meta0 = make_meta(e, m, 0, d->pt_stride, pos, sess, pt, d->c->p);
+    return launch_row_plan(e->stream, meta0, 1, (int32_t)m->kvdim, m->hd, m->cos_t, m->sin_t, kvoff,
+                           (float *)(kvoff + 1));
+}
+
+// One step: layers -> final norm + head -> the tail (argmax, advance, the
+// next step's embedding row and row plan).
 static int enqueue_decode_step(srq_decoder *d) {
     srq_exec *e = d->e;
     srq_model *m = d->m;
@@ -1276,13 +1296,37 @@ static int enqueue_decode_step(srq_decoder *d) {
     dm.sess = sess;
     dm.pages = pt;
     dm.pt_stride = d->pt_stride;
+    dm.plan_ready = true;
     Workspace &ws = d->ws;
-    SRQ_CHECK(launch_dequant_rows(e->stream, m->embed.fmt, m->c.dim, m->embed.values, m->embed.scales, embed_id, 1,
-                                  as<float>(ws.X)));
     SRQ_CHECK(enqueue_layers(e, ws, m, d->c->p, 1, d->start_pos + d->max_steps, dm, nullptr));
     SRQ_CHECK(enqueue_head(e, ws, m, as<float>(ws.X), 1));
-    SRQ_CHECK(launch_argmax(e->stream, as<float>(ws.LOGC), 1, m->c.vocab, token, err));
-    return launch_advance(e->stream, pos, token, outbuf, counter, embed_id);
+    const RowMeta meta0 = make_meta(e, m, 0, d->pt_stride, pos, sess, pt, d->c->p);
+    DecodeTailArgs t{};
+    t.logits = as<float>(ws.LOGC);
+    t.vocab = m->c.vocab;
+    t.token = token;
+    t.err = err;
+    t.pos = pos;
+    t.out = outbuf;
+    t.counter = counter;
+    t.embed_id = embed_id;
+    t.steps = d->max_steps;
+    t.fmt = m->embed.fmt;
+    t.values = m->embed.values;
+    t.scales = m->embed.scales;
+    t.dim = m->c.dim;
+    t.x = as<float>(ws.X);
+    t.sess = sess;
+    t.pages = pt;
+    t.pt_stride = d->pt_stride;
+    t.page_elems = meta0.page_elems;
+    t.kvdim = (int32_t)m->kvdim;
+    t.half = m->hd / 2;
+    t.cos_t = m->cos_t;
+    t.sin_t = m->sin_t;
+    t.kvoff = as<int64_t>(ws.PLAN);
+    t.rope_cs = (float *)(t.kvoff + 1);
+    return launch_decode_tail(e->stream, t);
 }
 
 int srq_decoder_create(srq_exec *e, srq_model *m, srq_cache *c, int32_t first_token, int32_t max_steps,
@@ -1331,10 +1375,16 @@ int srq_decoder_create(srq_exec *e, srq_model *m, srq_cache *c, int32_t first_to
         srq_decoder_destroy(d);
         return rc;
     }
-    // One decode step: embed -> layers -> final norm + head -> argmax ->
-    // record token, advance position.  Captured once as a HIP graph and
-    // replayed, unless the caller asked for eager launches.
+    // One decode step: layers -> final norm + head -> argmax -> record
+    // token, advance position, next step's embedding row and row plan.
+    // Captured once as a HIP graph and replayed, unless the caller asked for
+    // eager launches; the first step's input is prepared here.
     d->eager = (flags & SRQ_DECODER_EAGER) != 0;
+    rc = enqueue_decode_input(d);
+    if (rc != SRQ_OK) {
+        srq_decoder_destroy(d);
+        return rc;
+    }
     if (!d->eager) {
         if (hipStreamBeginCapture(e->stream, hipStreamCaptureModeThreadLocal) != hipSuccess) {
             srq_decoder_destroy(d);

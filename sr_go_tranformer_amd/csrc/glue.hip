@@ -111,8 +111,9 @@ __device__ __forceinline__ void arg_merge(float &best, int &idx, float ov, int o
     if (oi >= 0 && (idx < 0 || ov > best || (ov == best && oi < idx))) best = ov, idx = oi;
 }
 
-__global__ __launch_bounds__(kArgThreads) void argmax_kernel(const float *__restrict__ logits, int32_t vocab,
-                                                             int32_t *__restrict__ ids, int32_t *__restrict__ err) {
+// First maximum of one row by the whole 1024-thread workgroup; thread 0
+// gets the id (lowest on ties) and whether any value was non-finite.
+__device__ __forceinline__ void argmax_row(const float *__restrict__ row, int32_t vocab, int &id, int &nonfinite_any) {
     constexpr int NW = kArgThreads / 64, U = 8;
     __shared__ float bv[NW];
     __shared__ int bi[NW];
@@ -120,7 +121,6 @@ __global__ __launch_bounds__(kArgThreads) void argmax_kernel(const float *__rest
     const int tid = threadIdx.x;
     if (tid == 0) bad = 0;
     __syncthreads();
-    const float *row = logits + (int64_t)blockIdx.x * vocab;
     float best = 0.0f;
     int idx = -1;
     int nonfinite = 0;
@@ -172,21 +172,69 @@ __global__ __launch_bounds__(kArgThreads) void argmax_kernel(const float *__rest
         float b = bv[0];
         int i = bi[0];
         for (int w = 1; w < NW; ++w) arg_merge(b, i, bv[w], bi[w]);
-        ids[blockIdx.x] = i;
+        id = i;
+        nonfinite_any = bad;
+    }
+}
+
+__global__ __launch_bounds__(kArgThreads) void argmax_kernel(const float *__restrict__ logits, int32_t vocab,
+                                                             int32_t *__restrict__ ids, int32_t *__restrict__ err) {
+    int id = 0, bad = 0;
+    argmax_row(logits + (int64_t)blockIdx.x * vocab, vocab, id, bad);
+    if (threadIdx.x == 0) {
+        ids[blockIdx.x] = id;
         if (bad) err[0] = 1;
     }
 }
 
-// One decode step of a replayed greedy loop: record the token, feed it to
-// the next embedding lookup and advance the position.
-__global__ void advance_kernel(int32_t *pos, const int32_t *token, int32_t *out, int32_t *counter,
-                               int32_t *embed_ids) {
-    if (threadIdx.x == 0 && blockIdx.x == 0) {
-        const int t = token[0];
-        out[counter[0]] = t;
-        counter[0] = counter[0] + 1;
-        embed_ids[0] = t;
-        pos[0] = pos[0] + 1;
+// The tail of one step of a replayed greedy decoder, in one launch: the
+// argmax of the logits row (argmax_kernel's rule), the advance (token
+// recorded, counter and position + 1), and, while steps remain, the next
+// step's input: the token's embedding row (copyRow's f32(code) * scale,
+// M:3900-3921) and the row plan of the new position (row_plan_kernel's).
+template <int FMT>
+__global__ __launch_bounds__(kArgThreads) void decode_tail_kernel(const DecodeTailArgs A) {
+    __shared__ int tok, next_pos;
+    int id = 0, bad = 0;
+    argmax_row(A.logits, A.vocab, id, bad);
+    const int tid = threadIdx.x;
+    if (tid == 0) {
+        A.token[0] = id;
+        if (bad) A.err[0] = 1;
+        const int c = A.counter[0], p = A.pos[0] + 1;
+        A.out[c] = id;
+        A.counter[0] = c + 1;
+        A.embed_id[0] = id;
+        A.pos[0] = p;
+        tok = id;
+        next_pos = c + 1 < A.steps ? p : -1;
+    }
+    __syncthreads();
+    const int p = next_pos, r = tok;
+    if (p < 0) return;
+    const int64_t cols = A.dim, groups = groups_of(cols);
+    for (int64_t j = tid; j < cols; j += kArgThreads) {
+        if constexpr (FMT == SRQ_F32) {
+            A.x[j] = ((const float *)A.values)[(int64_t)r * cols + j];
+        } else {
+            float w;
+            if constexpr (FMT == SRQ_Q8) {
+                w = (float)((const int8_t *)A.values)[(int64_t)r * cols + j];
+            } else {
+                const uint32_t b = ((const uint8_t *)A.values)[(int64_t)r * ((cols + 1) / 2) + j / 2];
+                const uint32_t nib = (j & 1) ? (b >> 4) : (b & 15u);
+                w = (float)(((int32_t)(nib << 28)) >> 28);
+            }
+            A.x[j] = w * A.scales[(int64_t)r * groups + j / kBlock];
+        }
+    }
+    if (tid == 0) {
+        const int page = A.pages[(int64_t)A.sess[0] * A.pt_stride + p / kPageTokens];
+        A.kvoff[0] = (int64_t)page * A.page_elems + (int64_t)(p % kPageTokens) * A.kvdim;
+    }
+    for (int j = tid; j < A.half; j += kArgThreads) {
+        A.rope_cs[2 * j] = A.cos_t[(int64_t)p * A.half + j];
+        A.rope_cs[2 * j + 1] = A.sin_t[(int64_t)p * A.half + j];
     }
 }
 
@@ -263,16 +311,21 @@ int launch_gather_rows(hipStream_t s, const float *src, int64_t d, const int32_t
     return SRQ_OK;
 }
 
-int launch_argmax(hipStream_t s, const float *logits, int32_t rows, int32_t vocab, int32_t *ids, int32_t *err) {
-    if (rows <= 0) return SRQ_OK;
-    argmax_kernel<<<rows, kArgThreads, 0, s>>>(logits, vocab, ids, err);
+int launch_decode_tail(hipStream_t s, const DecodeTailArgs &a) {
+    if (a.vocab < 1 || a.dim < 1) return fail(SRQ_EINVAL, "decode tail: empty vocabulary or width");
+    if (a.fmt == SRQ_Q8)
+        decode_tail_kernel<SRQ_Q8><<<1, kArgThreads, 0, s>>>(a);
+    else if (a.fmt == SRQ_Q4)
+        decode_tail_kernel<SRQ_Q4><<<1, kArgThreads, 0, s>>>(a);
+    else
+        decode_tail_kernel<SRQ_F32><<<1, kArgThreads, 0, s>>>(a);
     SRQ_HIP(hipGetLastError());
     return SRQ_OK;
 }
 
-int launch_advance(hipStream_t s, int32_t *pos, const int32_t *token, int32_t *out, int32_t *counter,
-                   int32_t *embed_ids) {
-    advance_kernel<<<1, 64, 0, s>>>(pos, token, out, counter, embed_ids);
+int launch_argmax(hipStream_t s, const float *logits, int32_t rows, int32_t vocab, int32_t *ids, int32_t *err) {
+    if (rows <= 0) return SRQ_OK;
+    argmax_kernel<<<rows, kArgThreads, 0, s>>>(logits, vocab, ids, err);
     SRQ_HIP(hipGetLastError());
     return SRQ_OK;
 }

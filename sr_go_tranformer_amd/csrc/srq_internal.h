@@ -153,8 +153,29 @@ int launch_rope_kv(hipStream_t s, const float *qkv, const float *bias, int32_t n
 int launch_swiglu(hipStream_t s, const float *gu, int32_t n, int32_t hidden, float *h);
 int launch_gather_rows(hipStream_t s, const float *src, int64_t d, const int32_t *rows, int32_t count, float *dst);
 int launch_argmax(hipStream_t s, const float *logits, int32_t rows, int32_t vocab, int32_t *ids, int32_t *err);
-int launch_advance(hipStream_t s, int32_t *pos, const int32_t *token, int32_t *out, int32_t *counter,
-                   int32_t *embed_ids);
+// Tail of a replayed greedy decode step (one row): argmax of `logits` ->
+// token; out[counter] = token, counter + 1, embed_id = token, pos + 1; then,
+// if counter < steps, x = the token's embedding row and the row plan
+// (kvoff[0], rope_cs[0..head_dim)) of the new position.
+struct DecodeTailArgs {
+    const float *logits;
+    int32_t vocab;
+    int32_t *token, *err, *pos, *out, *counter, *embed_id;
+    int32_t steps;
+    int fmt;                   // embedding table
+    const void *values;
+    const float *scales;
+    int64_t dim;
+    float *x;
+    const int32_t *sess, *pages;  // row plan inputs (RowMeta's)
+    int32_t pt_stride;
+    int64_t page_elems;
+    int32_t kvdim, half;
+    const float *cos_t, *sin_t;
+    int64_t *kvoff;
+    float *rope_cs;
+};
+int launch_decode_tail(hipStream_t s, const DecodeTailArgs &a);
 // Row plan of a step's n rows: kvoff[r] = page*page_elems + (pos%32)*kvdim
 // and rope_cs[r] = {cos, sin} pairs of pos (tables [context x head_dim/2]).
 int launch_row_plan(hipStream_t s, const RowMeta &meta, int32_t n, int32_t kvdim, int32_t head_dim,
