@@ -354,6 +354,37 @@ __device__ __forceinline__ void merge_wave(const AttnArgs &A, const float *part,
     }
 }
 
+// Sum over splits i in [b0, b1) of cf[i] * pb[i * (hd + 4)] added to o by
+// FMA in split order, with two batches of kMergeBatch loads in flight (the
+// next batch loads while this one's FMAs run).
+__device__ __forceinline__ float merge_range(const float *pb, int hd, const float *cf, int b0, int b1, float o) {
+    if (b0 >= b1) return o;
+    const int64_t st = hd + 4;
+    const int last = b1 - 1;
+    float va[kMergeBatch], vb[kMergeBatch];
+#pragma unroll
+    for (int b = 0; b < kMergeBatch; ++b) va[b] = pb[(int64_t)min(b0 + b, last) * st];
+    for (int i0 = b0; i0 < b1; i0 += 2 * kMergeBatch) {
+        const int i1 = i0 + kMergeBatch;
+        if (i1 < b1) {
+#pragma unroll
+            for (int b = 0; b < kMergeBatch; ++b) vb[b] = pb[(int64_t)min(i1 + b, last) * st];
+        }
+#pragma unroll
+        for (int b = 0; b < kMergeBatch; ++b)
+            if (i0 + b < b1) o = __builtin_fmaf(cf[i0 + b], va[b], o);
+        if (i1 >= b1) break;
+        if (i1 + kMergeBatch < b1) {
+#pragma unroll
+            for (int b = 0; b < kMergeBatch; ++b) va[b] = pb[(int64_t)min(i1 + kMergeBatch + b, last) * st];
+        }
+#pragma unroll
+        for (int b = 0; b < kMergeBatch; ++b)
+            if (i1 + b < b1) o = __builtin_fmaf(cf[i1 + b], vb[b], o);
+    }
+    return o;
+}
+
 // Merge of split partials (m_i, l_i, o_i) for heads h0 .. h0+nh-1 of a row,
 // by all 256 threads of the workgroup:
 //   M = max_i m_i, l = sum_i l_i exp(m_i - M) (FP64), lse = M + log(l),
@@ -407,6 +438,13 @@ __device__ __forceinline__ void merge_splits(const AttnArgs &A, const float *par
     float o[kMergePairs];
 #pragma unroll
     for (int k = 0; k < kMergePairs; ++k) o[k] = 0.0f;
+    // Few (head, dim) pairs and many splits (one head of a long-context
+    // decode row): groups of threads take parts of the split range, so no
+    // thread idles.  Up to kFusedSplits splits the order stays the fused
+    // kernel's (one FMA chain per pair).
+    __shared__ float gs[256];
+    const int pairs = nh * hd;
+    const int ng = pairs <= 128 && 256 % pairs == 0 && used > kFusedSplits && used <= kMergeChunk ? 256 / pairs : 1;
     for (int c0 = 0; c0 < used; c0 += kMergeChunk) {
         const int cnt = min(kMergeChunk, used - c0);
         for (int t = tid; t < nh * cnt; t += 256) {
@@ -414,36 +452,28 @@ __device__ __forceinline__ void merge_splits(const AttnArgs &A, const float *par
             cf[g][i] = (float)exp((double)partial((float *)part, row, h0 + g, c0 + i, A.heads, nsplit, hd)[0] - lse[g]);
         }
         __syncthreads();
+        if (ng > 1) {
+            // Thread group q of ng sums splits [q*per, (q+1)*per) of its
+            // (head, dim) pair; the groups' sums are added in group order.
+            const int pidx = tid % pairs, q = tid / pairs, per = (cnt + ng - 1) / ng;
+            const int g = pidx / hd, j = pidx - g * hd;
+            const float *pb = partial((float *)part, row, h0 + g, c0, A.heads, nsplit, hd) + 4 + j;
+            gs[tid] = merge_range(pb, hd, cf[g], q * per, min(cnt, q * per + per), 0.0f);
+            __syncthreads();
+            if (q == 0) {
+                float v = gs[pidx];
+                for (int r = 1; r < ng; ++r) v += gs[r * pairs + pidx];
+                A.out[(int64_t)row * A.heads * hd + (int64_t)(h0 + g) * hd + j] = v;
+            }
+            return;
+        }
 #pragma unroll
         for (int k = 0; k < kMergePairs; ++k) {
             const int pidx = tid + 256 * k;
             if (pidx >= nh * hd) break;
             const int g = pidx / hd, j = pidx - g * hd;
             const float *pb = partial((float *)part, row, h0 + g, c0, A.heads, nsplit, hd) + 4 + j;
-            // Two batches in flight: the next batch loads while this one's
-            // FMAs (in split order) run.
-            float va[kMergeBatch], vb[kMergeBatch];
-#pragma unroll
-            for (int b = 0; b < kMergeBatch; ++b) va[b] = pb[(int64_t)min(b, cnt - 1) * (hd + 4)];
-            for (int i0 = 0; i0 < cnt; i0 += 2 * kMergeBatch) {
-                const int i1 = i0 + kMergeBatch;
-                if (i1 < cnt) {
-#pragma unroll
-                    for (int b = 0; b < kMergeBatch; ++b) vb[b] = pb[(int64_t)min(i1 + b, cnt - 1) * (hd + 4)];
-                }
-#pragma unroll
-                for (int b = 0; b < kMergeBatch; ++b)
-                    if (i0 + b < cnt) o[k] = __builtin_fmaf(cf[g][i0 + b], va[b], o[k]);
-                if (i1 >= cnt) break;
-                if (i1 + kMergeBatch < cnt) {
-#pragma unroll
-                    for (int b = 0; b < kMergeBatch; ++b)
-                        va[b] = pb[(int64_t)min(i1 + kMergeBatch + b, cnt - 1) * (hd + 4)];
-                }
-#pragma unroll
-                for (int b = 0; b < kMergeBatch; ++b)
-                    if (i1 + b < cnt) o[k] = __builtin_fmaf(cf[g][i1 + b], vb[b], o[k]);
-            }
+            o[k] = merge_range(pb, hd, cf[g], 0, cnt, o[k]);
         }
         __syncthreads();
     }
