@@ -726,7 +726,7 @@ __device__ __forceinline__ void unit_epilogue(const GemvArgs &A, const Unit &t, 
     }
 }
 
-template <int FMT, int NB, int EPI, bool NORM>
+template <int FMT, int NB, int EPI, bool NORM, bool WMAJOR>
 __global__ __launch_bounds__(kStreamThreads) void gemv_stream_kernel(const GemvArgs A) {
     using Ly = Lay<FMT, true>;
     constexpr int E = Ly::E, CW = Ly::CW, R = unit_rows_of<EPI>();
@@ -747,11 +747,15 @@ __global__ __launch_bounds__(kStreamThreads) void gemv_stream_kernel(const GemvA
     const int U = unit_count<EPI>(A);
     // Units are dealt round-robin (u = wid + k*nwaves): at any moment the
     // waves together sweep one contiguous band of rows, which spreads the
-    // traffic over every HBM channel.  Waves are numbered wave-major
-    // (wid = wave * workgroups + workgroup), so when the units do not divide
-    // evenly the extra ones land on every CU alike (q/k/v: 3072 units on
-    // 2048 waves give each CU 12, not 16 on half of them and 8 on the rest).
-    const int nwaves = (int)gridDim.x * kStreamWaves, wid = wave * (int)gridDim.x + (int)blockIdx.x;
+    // traffic over every HBM channel.  WMAJOR (rows of whole 1 KiB chunks):
+    // waves are numbered wave-major (wid = wave * workgroups + workgroup),
+    // so consecutive rows go to different CUs and XCDs, and when the units do
+    // not divide evenly the extra ones land on every CU alike (q/k/v: 3072
+    // units on 2048 waves give each CU 12, not 16 on half of them and 8 on
+    // the rest).  Shorter rows share cache lines with their neighbours and
+    // stay together on one CU (workgroup-major numbering).
+    const int nwaves = (int)gridDim.x * kStreamWaves;
+    const int wid = WMAJOR ? wave * (int)gridDim.x + (int)blockIdx.x : (int)blockIdx.x * kStreamWaves + wave;
     const int myunits = wid < U ? (U - 1 - wid) / nwaves + 1 : 0;
     const int steps = myunits * nch;
     const int ulast = wid + (myunits - 1) * nwaves;
@@ -953,7 +957,10 @@ int launch_t(hipStream_t s, const GemvArgs &a) {
         if ((units / (blocks * kStreamWaves) + 1) * nch >= (1LL << 31))
             return fail(SRQ_EINVAL, "gemv: %lld x %lld exceeds the per-wave step limit", (long long)a.rows,
                         (long long)a.cols);
-        gemv_stream_kernel<FMT, NB, EPI, NORM><<<(unsigned)blocks, kStreamThreads, lds, s>>>(a);
+        if (row_bytes(FMT, a.cols) % 1024 == 0)
+            gemv_stream_kernel<FMT, NB, EPI, NORM, true><<<(unsigned)blocks, kStreamThreads, lds, s>>>(a);
+        else
+            gemv_stream_kernel<FMT, NB, EPI, NORM, false><<<(unsigned)blocks, kStreamThreads, lds, s>>>(a);
         SRQ_HIP(hipGetLastError());
         return SRQ_OK;
     } else {
@@ -997,12 +1004,16 @@ hipError_t prepare_one() {
     if constexpr (NB > max_nb<FMT, FAST>()) {
         return hipSuccess;
     } else {
-        const void *f;
-        if constexpr (FAST)
-            f = (const void *)gemv_stream_kernel<FMT, NB, EPI, NORM>;
-        else
-            f = (const void *)gemv_kernel<FMT, false, NB, EPI, NORM>;
-        return hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMaxLds);
+        if constexpr (FAST) {
+            const hipError_t e = hipFuncSetAttribute((const void *)gemv_stream_kernel<FMT, NB, EPI, NORM, true>,
+                                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMaxLds);
+            if (e != hipSuccess) return e;
+            return hipFuncSetAttribute((const void *)gemv_stream_kernel<FMT, NB, EPI, NORM, false>,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMaxLds);
+        } else {
+            return hipFuncSetAttribute((const void *)gemv_kernel<FMT, false, NB, EPI, NORM>,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMaxLds);
+        }
     }
 }
 
