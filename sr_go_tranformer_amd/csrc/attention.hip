@@ -393,6 +393,7 @@ __device__ __forceinline__ float merge_range(const float *pb, int hd, const floa
 // butterfly); the (head, dim) pairs spread over the threads, each pair
 // keeping two batches of kMergeBatch splits in flight.  Up to 256 splits a
 // lane loads all its {m, l} in one round.
+template <bool GROUPS>
 __device__ __forceinline__ void merge_splits(const AttnArgs &A, const float *part, int nsplit, int row, int h0,
                                              int nh, int hd, int used, float (*cf)[kMergeChunk], double *lse) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -442,9 +443,12 @@ __device__ __forceinline__ void merge_splits(const AttnArgs &A, const float *par
     // decode row): groups of threads take parts of the split range, so no
     // thread idles.  Up to kFusedSplits splits the order stays the fused
     // kernel's (one FMA chain per pair).
-    __shared__ float gs[256];
+    // (GROUPS: the one-head combine; the many-head one never needs it.)
+    __shared__ float gs[GROUPS ? 256 : 1];
     const int pairs = nh * hd;
-    const int ng = pairs <= 128 && 256 % pairs == 0 && used > kFusedSplits && used <= kMergeChunk ? 256 / pairs : 1;
+    const int ng = GROUPS && pairs <= 128 && 256 % pairs == 0 && used > kFusedSplits && used <= kMergeChunk
+                       ? 256 / pairs
+                       : 1;
     for (int c0 = 0; c0 < used; c0 += kMergeChunk) {
         const int cnt = min(kMergeChunk, used - c0);
         for (int t = tid; t < nh * cnt; t += 256) {
@@ -452,7 +456,7 @@ __device__ __forceinline__ void merge_splits(const AttnArgs &A, const float *par
             cf[g][i] = (float)exp((double)partial((float *)part, row, h0 + g, c0 + i, A.heads, nsplit, hd)[0] - lse[g]);
         }
         __syncthreads();
-        if (ng > 1) {
+        if (GROUPS && ng > 1) {
             // Thread group q of ng sums splits [q*per, (q+1)*per) of its
             // (head, dim) pair; the groups' sums are added in group order.
             const int pidx = tid % pairs, q = tid / pairs, per = (cnt + ng - 1) / ng;
@@ -655,7 +659,7 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const AttnArgs A, con
     const int row = blockIdx.x, h = blockIdx.y;
     const int len = A.meta.pos[row] + 1;
     const int used = min(nsplit, (len + split_len - 1) / split_len);
-    merge_splits(A, part, nsplit, row, h, 1, A.head_dim, used, cf, lse);
+    merge_splits<true>(A, part, nsplit, row, h, 1, A.head_dim, used, cf, lse);
 }
 
 // The same for heads h0 .. h0+nh-1 of a row per workgroup (nh <= kMaxGroup):
@@ -667,7 +671,7 @@ __global__ __launch_bounds__(256) void attn_combine_heads_kernel(const AttnArgs 
     const int row = blockIdx.x, h0 = blockIdx.y * nh;
     const int len = A.meta.pos[row] + 1;
     const int used = min(nsplit, (len + split_len - 1) / split_len);
-    merge_splits(A, part, nsplit, row, h0, nh, A.head_dim, used, cf, lse);
+    merge_splits<false>(A, part, nsplit, row, h0, nh, A.head_dim, used, cf, lse);
 }
 
 // ------------------------------------------------------------ prefill
