@@ -221,6 +221,36 @@ def test_prefill_attention_tiles_match_oracle(ex, dim, heads, kv_heads):
         near(k, np.stack([oa.row(layer, p, 0) for p in range(660)]))
 
 
+def test_wide_rows_through_fused_reductions(ex):
+    """A value projection scaled to ~1e34 makes the attention output exceed
+    f32(MaxFloat32/(2*64*127)) (M:4346-4354), so the o projection of a
+    40-row step (split-K MFMA GEMM, residual and RMSNorm in its reduction)
+    computes those rows in FP64 (linearQ8WideInto, M:4356-4382).  Logits and
+    K/V rows against the oracle's step."""
+    cfg = srq.make_config(300, 512, 2, 4, 1, 512, 1400, 10000.0, 1e-5, True)
+    m, norms = gpu_models.synthetic(ex, cfg, "q8", 21)
+    kvdim = cfg.dim // cfg.heads * cfg.kv_heads
+    v = (np.random.default_rng(5).normal(0.0, 0.02, size=(kvdim, cfg.dim)) * 1e36).astype(np.float32)
+    m.load(srq.T_V, 0, v)
+    om = gpu_models.oracle_from_device(ex, m, cfg, norms)
+    ids = [int(t) for t in np.random.default_rng(6).integers(0, cfg.vocab, size=45)]
+    pool = m.pool(8)
+    c, oc = pool.cache(4), om.new_cache()
+    got = m.step([c], [ids[:40]])[0]
+    want = om.step([oc], [ids[:40]])[0]
+    assert np.all(np.isfinite(got))
+    near(got, want)
+    # the next rows (a 5-row step: the streaming GEMV's FP64 pass)
+    near(m.step([c], [ids[40:]])[0], om.step([oc], [ids[40:]])[0])
+    # V rows of ~1e35: an entry near cancellation carries the f32 rounding of
+    # its ~1e35 terms, so the bound is relative to the row's largest entry.
+    for layer in range(cfg.layers):
+        k, vv = c.read(layer, 0, 45)
+        want_v = np.stack([oc.row(layer, p, 1) for p in range(45)]).astype(np.float64)
+        bound = 1e-4 * np.abs(want_v).max(axis=1, keepdims=True)
+        assert np.all(np.abs(vv.astype(np.float64) - want_v) <= bound), layer
+
+
 def test_smollm2_shape_greedy_identity(ex):
     """SmolLM2-135M architecture (576 / 30 layers / 9:3 heads / 1536 /
     49152 tied), seeded N(0, 0.02) weights, Q8; 32-token prompt (one MFMA
