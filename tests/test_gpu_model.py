@@ -221,6 +221,37 @@ def test_prefill_attention_tiles_match_oracle(ex, dim, heads, kv_heads):
         near(k, np.stack([oa.row(layer, p, 0) for p in range(660)]))
 
 
+@pytest.mark.parametrize("dim,heads,kv_heads", [(512, 4, 1), (1024, 8, 2)])
+def test_qkv_bias_through_fused_rope_reduction(ex, dim, heads, kv_heads):
+    """q/k/v biases (the Qwen2 profile) on split-K q/k/v GEMMs: the split
+    reduction adds the bias, applies RoPE and writes K/V (rope_kv_kernel's
+    arithmetic, M:3933-3940, M:5264-5289).  Logits and every K/V row of
+    40- and 33-row steps, then a 3-row GEMV step, against the oracle."""
+    print("qkv bias", dim, heads, kv_heads, flush=True)
+    cfg = srq.make_config(300, dim, 2, heads, kv_heads, 512, 1400, 10000.0, 1e-5, True, qkv_bias=True)
+    m, norms = gpu_models.synthetic(ex, cfg, "q8", 31)
+    kvdim = dim // heads * kv_heads
+    rng = np.random.default_rng(dim + heads)
+    for layer in range(cfg.layers):
+        for kind, name, width in ((srq.T_Q_BIAS, "q_bias", dim), (srq.T_K_BIAS, "k_bias", kvdim),
+                                  (srq.T_V_BIAS, "v_bias", kvdim)):
+            b = rng.normal(0.0, 0.5, size=width).astype(np.float32)
+            m.load(kind, layer, b)
+            norms["layers.%d.%s" % (layer, name)] = b
+    om = gpu_models.oracle_from_device(ex, m, cfg, norms)
+    ids = [int(t) for t in rng.integers(0, cfg.vocab, size=76)]
+    pool = m.pool(8)
+    c, oc = pool.cache(4), om.new_cache()
+    lo = 0
+    for n in (40, 33, 3):
+        near(m.step([c], [ids[lo:lo + n]])[0], om.step([oc], [ids[lo:lo + n]])[0])
+        lo += n
+    for layer in range(cfg.layers):
+        k, v = c.read(layer, 0, lo)
+        near(k, np.stack([oc.row(layer, p, 0) for p in range(lo)]))
+        near(v, np.stack([oc.row(layer, p, 1) for p in range(lo)]))
+
+
 def test_wide_rows_through_fused_reductions(ex):
     """A value projection scaled to ~1e34 makes the attention output exceed
     f32(MaxFloat32/(2*64*127)) (M:4346-4354), so the o projection of a
