@@ -651,7 +651,10 @@ __global__ __launch_bounds__(256) void attn_fused_kernel(const AttnArgs A, float
 }
 
 // lse and the weighted sum of split partials for one (row, head); split i
-// covers positions [i*split_len, (i+1)*split_len).
+// covers positions [i*split_len, (i+1)*split_len).  GROUPS (decode-sized
+// batches): thread groups share a head's split range; larger batches keep
+// the smaller register footprint, many workgroups being resident anyway.
+template <bool GROUPS>
 __global__ __launch_bounds__(256) void attn_combine_kernel(const AttnArgs A, const float *__restrict__ part,
                                                            int nsplit, int split_len) {
     __shared__ float cf[kMaxGroup][kMergeChunk];
@@ -659,7 +662,7 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const AttnArgs A, con
     const int row = blockIdx.x, h = blockIdx.y;
     const int len = A.meta.pos[row] + 1;
     const int used = min(nsplit, (len + split_len - 1) / split_len);
-    merge_splits<true>(A, part, nsplit, row, h, 1, A.head_dim, used, cf, lse);
+    merge_splits<GROUPS>(A, part, nsplit, row, h, 1, A.head_dim, used, cf, lse);
 }
 
 // The same for heads h0 .. h0+nh-1 of a row per workgroup (nh <= kMaxGroup):
@@ -914,7 +917,10 @@ int launch_attention(hipStream_t s, const AttnArgs &a, float *scratch, int32_t *
     else
         attn_split_kernel<<<grid, 256, 0, s>>>(a, scratch, nsplit);
     SRQ_HIP(hipGetLastError());
-    attn_combine_kernel<<<dim3(a.n, a.heads), 256, 0, s>>>(a, scratch, nsplit, kSplit);
+    if (a.n <= kFusedRows)
+        attn_combine_kernel<true><<<dim3(a.n, a.heads), 256, 0, s>>>(a, scratch, nsplit, kSplit);
+    else
+        attn_combine_kernel<false><<<dim3(a.n, a.heads), 256, 0, s>>>(a, scratch, nsplit, kSplit);
     SRQ_HIP(hipGetLastError());
     return SRQ_OK;
 }

@@ -221,15 +221,15 @@ def test_prefill_attention_tiles_match_oracle(ex, dim, heads, kv_heads):
         near(k, np.stack([oa.row(layer, p, 0) for p in range(660)]))
 
 
-@pytest.mark.parametrize("dim,heads,kv_heads", [(512, 4, 1), (1024, 8, 2)])
-def test_qkv_bias_through_fused_rope_reduction(ex, dim, heads, kv_heads):
+@pytest.mark.parametrize("dim,heads,kv_heads,fmt", [(512, 4, 1, "q8"), (1024, 8, 2, "q8"), (1024, 8, 2, "q4")])
+def test_qkv_bias_through_fused_rope_reduction(ex, dim, heads, kv_heads, fmt):
     """q/k/v biases (the Qwen2 profile) on split-K q/k/v GEMMs: the split
     reduction adds the bias, applies RoPE and writes K/V (rope_kv_kernel's
     arithmetic, M:3933-3940, M:5264-5289).  Logits and every K/V row of
     40- and 33-row steps, then a 3-row GEMV step, against the oracle."""
-    print("qkv bias", dim, heads, kv_heads, flush=True)
+    print("qkv bias", dim, heads, kv_heads, fmt, flush=True)
     cfg = srq.make_config(300, dim, 2, heads, kv_heads, 512, 1400, 10000.0, 1e-5, True, qkv_bias=True)
-    m, norms = gpu_models.synthetic(ex, cfg, "q8", 31)
+    m, norms = gpu_models.synthetic(ex, cfg, fmt, 31)
     kvdim = dim // heads * kv_heads
     rng = np.random.default_rng(dim + heads)
     for layer in range(cfg.layers):
