@@ -553,8 +553,49 @@ struct StreamSmem {
 // (a = f32(1/sqrt(Sum f64(x^2)/d + eps)), y = (x*a)*w, M:6182-6194) and flag
 // rows holding |x| > kWideLimit.  One batched pass of global loads, then
 // LDS-only work.  Every thread of the workgroup calls it; ends with a barrier.
+// Workgroup barrier over LDS only: it waits for this wave's LDS traffic but
+// not for its global loads, so a weight prefetch issued before it keeps
+// streaming across it (a __syncthreads() waits for every load in flight).
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// One pass of the activation staging held in registers: float4 loads of 8
+// rows' worth per thread, so one pass stages a 16384-column single row (the
+// 14336-wide down input).  The first pass is issued before the weight
+// prefetch, so staging waits only for its own loads (global loads complete
+// in issue order).
+template <int NB, bool NORM>
+struct StagePass {
+    static constexpr int U = NB >= 8 ? 1 : 8 / NB;
+    float4 t[NB][U], w[U];
+};
+
+template <bool NORM>
+__device__ __forceinline__ bool stage_vec(const GemvArgs &A) {
+    return ((((uintptr_t)A.x) | (NORM ? (uintptr_t)A.norm_w : 0)) & 15) == 0 && (A.cols & 3) == 0;
+}
+
+template <int NB, bool NORM>
+__device__ __forceinline__ void stage_pass_load(const GemvArgs &A, int c0, StagePass<NB, NORM> &s) {
+    constexpr int U = StagePass<NB, NORM>::U;
+    const int cols = (int)A.cols;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int c = c0 + u * kStreamThreads * 4;
+#pragma unroll
+        for (int b = 0; b < NB; ++b)
+            s.t[b][u] = (b < A.n && c < cols) ? *(const float4 *)(A.x + (int64_t)b * cols + c)
+                                              : make_float4(0.f, 0.f, 0.f, 0.f);
+        if (NORM) s.w[u] = c < cols ? *(const float4 *)(A.norm_w + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+}
+
 template <int E, int CW, int NB, int EPI, bool NORM>
-__device__ __forceinline__ void stage_stream(const GemvArgs &A, float *lds, const StreamLds &L, StreamSmem &sm) {
+__device__ __forceinline__ void stage_stream(const GemvArgs &A, float *lds, const StreamLds &L, StreamSmem &sm,
+                                             bool vec, StagePass<NB, NORM> &sp) {
     constexpr int NT = kStreamThreads, NW = kStreamWaves;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int cols = (int)A.cols, ld = L.ld;
@@ -574,22 +615,13 @@ __device__ __forceinline__ void stage_stream(const GemvArgs &A, float *lds, cons
     double ss[NB];
 #pragma unroll
     for (int b = 0; b < NB; ++b) ss[b] = 0.0;
-    const bool vec = ((((uintptr_t)A.x) | (NORM ? (uintptr_t)A.norm_w : 0)) & 15) == 0 && (cols & 3) == 0;
     if (vec) {
-        // float4 loads in flight per thread: 8 rows' worth, so one pass
-        // stages a 16384-column single row (the 14336-wide down input).
-        constexpr int U = NB >= 8 ? 1 : 8 / NB;
+        // The first pass (c0 = tid * 4) is already in sp.
+        constexpr int U = StagePass<NB, NORM>::U;
         for (int c0 = tid * 4; c0 < ld; c0 += NT * 4 * U) {
-            float4 t[NB][U], w[U];
-#pragma unroll
-            for (int u = 0; u < U; ++u) {
-                const int c = c0 + u * NT * 4;
-#pragma unroll
-                for (int b = 0; b < NB; ++b)
-                    t[b][u] = (b < A.n && c < cols) ? *(const float4 *)(A.x + (int64_t)b * cols + c)
-                                                    : make_float4(0.f, 0.f, 0.f, 0.f);
-                if (NORM) w[u] = c < cols ? *(const float4 *)(A.norm_w + c) : make_float4(0.f, 0.f, 0.f, 0.f);
-            }
+            if (c0 != tid * 4) stage_pass_load<NB, NORM>(A, c0, sp);
+            const auto &t = sp.t;
+            const auto &w = sp.w;
 #pragma unroll
             for (int u = 0; u < U; ++u) {
                 const int c = c0 + u * NT * 4;
@@ -624,14 +656,14 @@ __device__ __forceinline__ void stage_stream(const GemvArgs &A, float *lds, cons
             if (lane == 0) sm.ss[b][wave] = t;
         }
     }
-    __syncthreads();
+    lds_barrier();
     if (NORM) {
         if (tid < NB) {
             double t = 0.0;
             for (int w = 0; w < NW; ++w) t += sm.ss[tid][w];
             sm.a[tid] = (float)(1.0 / sqrt(t / (double)cols + A.norm_eps));
         }
-        __syncthreads();
+        lds_barrier();
     }
     // LDS only: normalise ((x*a)*w, unfused) and flag wide rows.  cols is a
     // multiple of 4 for every streaming layout.
@@ -658,7 +690,7 @@ __device__ __forceinline__ void stage_stream(const GemvArgs &A, float *lds, cons
             sm.any_wide = 1;
         }
     }
-    __syncthreads();
+    lds_barrier();
 }
 
 // Write one unit's results: lane b (b < NB, b < n, write) stores batch
@@ -745,6 +777,7 @@ __global__ __launch_bounds__(kStreamThreads) void gemv_stream_kernel(const GemvA
 
     const int64_t rb = row_bytes(FMT, cols), sgroups = groups_of(cols);
     const int U = unit_count<EPI>(A);
+    if (U == 0) return;  // grid-uniform: no rows, nothing to load or write
     // Units are dealt round-robin (u = wid + k*nwaves): at any moment the
     // waves together sweep one contiguous band of rows, which spreads the
     // traffic over every HBM channel.  WMAJOR (rows of whole 1 KiB chunks):
@@ -810,14 +843,22 @@ __global__ __launch_bounds__(kStreamThreads) void gemv_stream_kernel(const GemvA
             set_rows(lu);
         }
     };
-    if (steps > 0) {
-        set_rows(wid);
-        // Weight loads do not depend on x: start them before staging it.
+    // The first staging pass is issued first; the weight prefetch, which
+    // does not depend on x, follows and streams through the staging.
+    const bool svec = stage_vec<NORM>(A);
+    StagePass<NB, NORM> sp;
+    if (svec) stage_pass_load<NB, NORM>(A, tid * 4, sp);
+    // Every wave issues the prefetch, so it is straight-line code and the
+    // compiler waits for the staging loads alone; a wave with no unit
+    // re-reads unit 0's first chunks and discards them.
+    set_rows(steps > 0 ? wid : 0);
 #pragma unroll
-        for (int p = 0; p < P; ++p) load_next(wb[p], sb[p], eb[p]);
+    for (int p = 0; p < P; ++p) load_next(wb[p], sb[p], eb[p]);
+    stage_stream<E, CW, NB, EPI, NORM>(A, lds, L, sm, svec, sp);
+    if (steps == 0) {  // wave-uniform; no barrier follows
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): no load outlives the wave
+        return;
     }
-    stage_stream<E, CW, NB, EPI, NORM>(A, lds, L, sm);
-    if (steps == 0) return;  // wave-uniform; no barrier follows
     // Batch rows flagged wide are written by the FP64 pass below instead.
     const bool fast_row = !(lane < NB && sm.wide[lane]);
 
