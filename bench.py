@@ -97,6 +97,7 @@ def gemv_roofline(srq, ex, weights, hip, launches, label):
     algo = vb + sb + cols * 4 + rows * 4
     avg_s = ms / 1e3 / launches
     achieved = algo / avg_s / 1e9
+    prof_us = read_profile_avg_us("gemv_q8_%dx%d_kernel_trace.txt" % (rows, cols))
     return {
         "kernel": "gemv_stream_kernel<Q8, n=1, plain> %dx%d (%s)" % (rows, cols, label),
         "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
@@ -104,6 +105,11 @@ def gemv_roofline(srq, ex, weights, hip, launches, label):
         "traffic": read_traffic("gemv_q8_%dx%d_pmc.txt" % (rows, cols)),
         "algorithmic_bytes_per_launch": algo, "avg_launch_us": round(avg_s * 1e6, 3),
         "launches": launches,
+        # the committed rocprofv3 summary of the standalone leg (its tracer
+        # adds a little per dispatch): same bytes over its average duration
+        "profile": None if prof_us is None else {
+            "file": "profiles/gemv_q8_%dx%d_kernel_trace.txt" % (rows, cols), "avg_kernel_us": prof_us,
+            "frac": round(algo / (prof_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)},
     }
 
 
@@ -131,6 +137,19 @@ def gemv_only(srq, launches, seed, rows):
     ex.synchronize()
     print(json.dumps({"roofline": roof, "calibration_copy_bytes": copy_bytes}), flush=True)
     return 0
+
+
+def read_profile_avg_us(name, kernel_prefix="void gemv_stream_kernel<1, 1, 0, false, true>"):
+    """Average duration (us) of the roofline kernel in a committed rocprofv3
+    --kernel-trace --stats summary."""
+    path = os.path.join(ROOT, "profiles", name)
+    try:
+        for line in open(path):
+            if line.strip().startswith(kernel_prefix):
+                return float(line.split()[-3])
+    except (OSError, ValueError, IndexError):
+        pass
+    return None
 
 
 def read_traffic(name):
@@ -180,7 +199,7 @@ def cpu_baseline(srq, ex, model, cfg, cache, first, gpu_tokens, n_tokens):
     runs = []
     # All host cores (16 at most: the GPU box's CPU share), then 4 threads,
     # the GOMAXPROCS of the reference's published receipts.
-    for workers, count in ((min(os.cpu_count() or 1, 16), n_tokens), (4, max(1, n_tokens // 2))):
+    for workers, count in ((min(os.cpu_count() or 1, 16), n_tokens), (4, max(1, n_tokens // 4))):
         oc.set_pos(PROMPT)
         t0 = time.perf_counter()
         produced = []
@@ -190,6 +209,19 @@ def cpu_baseline(srq, ex, model, cfg, cache, first, gpu_tokens, n_tokens):
         runs.append((workers, count / (time.perf_counter() - t0), produced))
     om.close()
     return runs, setup_s
+
+
+def host_facts():
+    """nproc and CPU model of the host the CPU baseline runs on."""
+    model = None
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"nproc": os.cpu_count(), "cpu_model": model or os.uname().machine}
 
 
 def percentiles(us):
@@ -344,30 +376,6 @@ def bench_q4mixed_prefill(srq, args):
     return 0
 
 
-def schedule_tokens(remaining, decoding, budget, chunk, mixed_chunk, start):
-    """scheduleTokens (M:8180-8210): one row per active session, then extra
-    prefill rows round-robin from `start` up to min(chunk, remaining) each
-    (chunk capped at mixed_chunk while any session decodes) within `budget`."""
-    n = len(remaining)
-    if any(decoding):
-        chunk = min(chunk, mixed_chunk)
-    counts = [1] * n
-    total = n
-    while total < budget:
-        progress = False
-        for j in range(n):
-            i = (start + j) % n
-            if counts[i] < min(chunk, remaining[i]):
-                counts[i] += 1
-                total += 1
-                progress = True
-                if total == budget:
-                    break
-        if not progress:
-            break
-    return counts
-
-
 def bench_continuous_batching(srq, args):
     """Llama-3.2-3B shape (3072 / 28 layers / 24:8 heads / 8192 / 128256
     tied), Q8, seeded N(0, 0.02) weights: 32 concurrent requests, prompt
@@ -376,6 +384,7 @@ def bench_continuous_batching(srq, args):
     budget 64), sampling at temperature 0.8, top-p 0.9, top-k off, no repeat
     penalty, RNG{seed + i} per request; logits stay on the device."""
     from sr_go_tranformer_amd import synthetic
+    from sr_go_tranformer_amd.schedule import TickPlanner
     sessions_n, out_n, budget, chunk, mixed = 32, args.gen_tokens_cb, 64, 16, 1
     r = synthetic.SplitMix64(args.seed)
     lens = [64 + r.intn(1024 - 64 + 1) for _ in range(sessions_n)]
@@ -386,51 +395,34 @@ def bench_continuous_batching(srq, args):
     pages = sum((n + out_n + 31) // 32 for n in lens)
     pool = model.pool(pages + 8)
     caches = [pool.cache((n + out_n + 31) // 32) for n in lens]
-    cursor = [0] * sessions_n
-    outputs = [[] for _ in range(sessions_n)]
     rng = np.array([(args.seed + i) & ((1 << 64) - 1) for i in range(sessions_n)], np.uint64)
     params = srq.Sampling(0.8, 0, 0.9, 1.0)
-    active = list(range(sessions_n))
-    steps, rows_total, start = 0, 0, 0
+    tp = TickPlanner(prompts, out_n, budget, chunk, mixed)
+    steps, rows_total = 0, 0
     ex.synchronize()
     t0 = time.perf_counter()
-    while active:
-        remaining = [len(prompts[i]) - cursor[i] for i in active]
-        decoding = [rem == 0 for rem in remaining]
-        counts = schedule_tokens(remaining, decoding, budget, chunk, mixed, start)
-        start += 1
-        chunks, want = [], []
-        for k, i in enumerate(active):
-            if decoding[k]:
-                chunks.append([outputs[i][-1]])
-                want.append(True)
-            else:
-                c = counts[k]
-                chunks.append(prompts[i][cursor[i]:cursor[i] + c])
-                want.append(cursor[i] + c == len(prompts[i]))
-        dev = model.step([caches[i] for i in active], chunks, want=want, host=False)
+    while not tp.done():
+        sessions, chunks, want = tp.plan()
+        dev = model.step([caches[i] for i in sessions], chunks, want=want, host=False)
         rows_total += sum(len(c) for c in chunks)
         steps += 1
-        sel = [k for k in range(len(active)) if want[k]]
+        sel = [k for k in range(len(sessions)) if want[k]]
+        sampled = {}
         if sel:
             # the step's logits are [sessions x vocab]; sample the rows of the
             # sessions that asked for a token
-            st = rng[[active[k] for k in sel]].copy()
+            st = rng[[sessions[k] for k in sel]].copy()
             ids = srq.sample(ex, dev, len(sel), cfg.vocab, params, st, row_ids=sel)
             for j, k in enumerate(sel):
-                i = active[k]
-                rng[i] = st[j]
-                outputs[i].append(int(ids[j]))
-        for k, i in enumerate(active):
-            if not decoding[k]:
-                cursor[i] += len(chunks[k])
-        done = [i for i in active if len(outputs[i]) >= out_n]
-        for i in done:
+                rng[sessions[k]] = st[j]
+                sampled[sessions[k]] = int(ids[j])
+        live = set(tp.live)
+        tp.commit(sampled)
+        for i in live - set(tp.live):
             caches[i].close()
-        active = [i for i in active if len(outputs[i]) < out_n]
     ex.synchronize()
     dt = time.perf_counter() - t0
-    gen = sum(len(o) for o in outputs)
+    gen = sum(len(o) for o in tp.outputs)
     print(json.dumps({
         "metric": "Llama-3.2-3B-shape Q8 continuous batching output tokens/s (32 requests)",
         "value": round(gen / dt, 1), "unit": "tokens/s", "n_gpus": 1, "higher_is_better": True, "dtype": "f32",
@@ -593,7 +585,7 @@ def main():
     ap.add_argument("--steps", type=int, default=240, help="timed decode tokens")
     ap.add_argument("--warmup", type=int, default=15, help="untimed decode tokens")
     ap.add_argument("--seed", type=int, default=1)
-    ap.add_argument("--cpu-tokens", type=int, default=6, help="decode tokens of the CPU baseline sample")
+    ap.add_argument("--cpu-tokens", type=int, default=32, help="decode tokens of the CPU baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--gemv-launches", type=int, default=320)
     ap.add_argument("--config", default="mistral7b-q8-decode",
@@ -695,18 +687,22 @@ def main():
 
     cpu = None
     if not args.no_cpu_baseline:
-        n = max(1, args.cpu_tokens)
+        # the oracle decodes the GPU's own token sequence (first + replays)
+        n = max(1, min(args.cpu_tokens, len(tokens)))
         runs, setup_s = cpu_baseline(srq, ex, model, cfg, cache, first, tokens, n)
         (workers, tps, produced), (w4, tps4, produced4) = runs
+        host = host_facts()
         cpu = {"value": round(wbytes * tps / 1e9, 3), "unit": "GB/s", "tokens_per_s": round(tps, 4),
                "cores": workers, "kind": "port",
                "sample": "%d greedy decode tokens of the same Mistral-7B-shape Q8 model from position %d "
                          "(KV rows copied from the GPU prefill), oracle C restatement of the reference Go "
-                         "CPU path, %d worker threads (GOMAXPROCS-equivalent), %s" %
-                         (n, PROMPT, workers, os.uname().machine),
+                         "CPU path, %d worker threads (GOMAXPROCS-equivalent) on a %d-CPU host (%s)" %
+                         (n, PROMPT, workers, host["nproc"], host["cpu_model"]),
+               "nproc": host["nproc"], "cpu_model": host["cpu_model"], "gomaxprocs_equivalent": workers,
                "greedy_match": produced == tokens[:len(produced)],
                "threads_4": {"value": round(wbytes * tps4 / 1e9, 3), "tokens_per_s": round(tps4, 4),
-                             "tokens": len(produced4), "greedy_match": produced4 == tokens[:len(produced4)]}}
+                             "tokens": len(produced4), "gomaxprocs_equivalent": 4,
+                             "greedy_match": produced4 == tokens[:len(produced4)]}}
         print("cpu %.3f tok/s (%d threads), %.3f tok/s (4 threads)" % (tps, workers, tps4), file=sys.stderr,
               flush=True)
 
@@ -724,10 +720,13 @@ def main():
         "dtype": "f32",
         "data": "synthetic",
         "config": {
-            "workload": "Mistral-7B-shape Q8 greedy decode, batch 1, 128-token random prompt, 256 tokens",
+            "workload": "Mistral-7B-shape Q8 greedy decode, batch 1, 128-token random prompt, %d greedy tokens "
+                        "(the first from the prefill, %d untimed and %d timed graph-replayed decode steps)" %
+                        (1 + args.warmup + args.steps, args.warmup, args.steps),
             "hidden": cfg.dim, "layers": cfg.layers, "heads": cfg.heads, "kv_heads": cfg.kv_heads,
             "intermediate": cfg.hidden, "vocab": cfg.vocab, "page_tokens": 32, "weights": "int8 Q8, f32 scales/64",
-            "prompt_tokens": PROMPT, "generated_tokens": TOKENS, "seed": args.seed,
+            "prompt_tokens": PROMPT, "generated_tokens": 1 + args.warmup + args.steps, "timed_tokens": args.steps,
+            "seed": args.seed,
             "decode_launch": "eager" if args.eager else "hip-graph",
             "vs_baseline_reference": "Mistral-7B Q8 decode batch 1 on Apple M4 (GOMAXPROCS=4): 1.33 tok/s, "
                                      "10.1 GB/s of weights",

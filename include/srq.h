@@ -114,9 +114,12 @@ int srq_dequant_rows(srq_exec *e, const srq_weight *w, const int32_t *rows, int3
 /* y[n x w.rows] = x[n x w.cols] . W^T; x, y device, disjoint; n 1..1024.
  * Q8 / Q4 / F32 dispatch as the reference.  Rows holding any |x| above
  * MaxFloat32/(2*64*127) take an FP64 path (M:4346-4382), chosen per row.
- * Results are deterministic and independent of a row's position in the
- * batch; for n <= 16 they are also bit-identical to the row computed
- * alone. */
+ * Results are deterministic, and a row's bits depend on neither its
+ * position in the batch nor on n within each of the two paths: n <= 16
+ * takes the GEMV (bit-identical to the row computed alone), n > 16 the MFMA
+ * GEMM (bit-identical for every n > 16; its split-K plan depends on the
+ * matrix shape only).  The two paths differ in rounding (both within 1e-4
+ * of the reference). */
 int srq_linear(srq_exec *e, float *y, const float *x, const srq_weight *w, int32_t n);
 /* Same computation, stream-ordered on the executor without joining: for
  * callers that chain work on the executor's stream (or time it with HIP
@@ -211,7 +214,8 @@ int srq_cache_read(srq_exec *e, const srq_cache *c, int32_t layer, int32_t pos0,
 /* Appends chunk_lens[i] tokens (host, concatenated in tokens) to caches[i]
  * for 1..256 sessions, at most 1024 rows in total, and returns last-row
  * logits per session in *logits (device, [sessions x vocab], borrowed until
- * the executor's next step).  want (host, nullable) selects sessions whose
+ * the executor's next step).  A cache owned by a live srq_decoder is
+ * rejected (SRQ_EINVAL).  want (host, nullable) selects sessions whose
  * logits are computed; unselected rows are zeroed (M:6438-6448).  Every
  * argument is validated before anything is mutated; positions are committed
  * only on success.  cancel (host, nullable) is polled between layers:
@@ -259,9 +263,12 @@ int srq_sample(srq_exec *e, const float *logits, int32_t rows, const int32_t *ro
  * head -> device argmax -> next token) as a HIP graph.  run: enqueues
  * `steps` replays without joining (each replay commits one position).
  * tokens: joins, copies the tokens produced so far (host, [steps run]) and
- * commits the cache position; SRQ_ENONFINITE if any logits were not finite.
- * The decoder owns its workspace; the cache must not be stepped elsewhere
- * while a decoder on it is alive. */
+ * commits the cache position.  If a step's logits were not finite it
+ * returns SRQ_ENONFINITE with *count = the tokens before that step, and the
+ * position committed through that step (inferHFIDs, M:1212-1238); replays
+ * after it are discarded.  The decoder owns its workspace and, while it
+ * lives, its cache: srq_step and a second srq_decoder_create on that cache
+ * fail with SRQ_EINVAL until srq_decoder_destroy. */
 typedef struct srq_decoder srq_decoder;
 /* flags: SRQ_DECODER_EAGER launches every kernel of each step directly
  * instead of replaying a captured graph (for tracers that cannot follow
@@ -276,7 +283,8 @@ int srq_decoder_destroy(srq_decoder *d);
 /* inferHFIDs (M:1185-1240): prefill ids in chunk-token steps, then count
  * greedy tokens (decode steps replayed as one HIP graph, argmax on device).
  * eos < 0 disables the EOS stop.  out_tokens (host) [count]; *produced
- * receives the number of tokens written. */
+ * receives the number of tokens written, also when a step's logits are not
+ * finite (SRQ_ENONFINITE: the tokens before that step). */
 int srq_generate_greedy(srq_exec *e, srq_model *m, srq_cache *c, const int32_t *ids, int32_t n_ids,
                         int32_t chunk, int32_t count, int32_t eos, int32_t *out_tokens, int32_t *produced);
 

@@ -391,8 +391,14 @@ class Model:
         ids = np.asarray(ids, np.int32)
         out = np.zeros(count, np.int32)
         produced = C.c_int32()
-        check(lib().srq_generate_greedy(self.ex.h, self.h, cache.h, _np_ptr(ids), len(ids), chunk, count, eos,
-                                        _np_ptr(out), C.byref(produced)))
+        rc = lib().srq_generate_greedy(self.ex.h, self.h, cache.h, _np_ptr(ids), len(ids), chunk, count, eos,
+                                       _np_ptr(out), C.byref(produced))
+        if rc != OK:
+            try:
+                check(rc)
+            except SrqError as e:
+                e.tokens = out[:produced.value].tolist()
+                raise
         return out[:produced.value].tolist()
 
     def close(self):
@@ -508,9 +514,17 @@ class Decoder:
         check(lib().srq_decoder_run(self.h, steps))
 
     def tokens(self):
+        """Tokens produced so far.  On SRQ_ENONFINITE the SrqError carries
+        the tokens before the failing step as .tokens."""
         out = np.zeros(self.max_steps, np.int32)
         n = C.c_int32()
-        check(lib().srq_decoder_tokens(self.h, _np_ptr(out), C.byref(n)))
+        rc = lib().srq_decoder_tokens(self.h, _np_ptr(out), C.byref(n))
+        if rc != OK:
+            try:
+                check(rc)
+            except SrqError as e:
+                e.tokens = out[:n.value].tolist()
+                raise
         return out[:n.value].tolist()
 
     def close(self):

@@ -191,6 +191,7 @@ struct srq_cache {
     int32_t pos = 0, reserve = 0;
     std::vector<int32_t> pages;
     bool released = false;
+    bool busy = false;  // a live decoder owns the cache's position and rows
 };
 
 namespace {
@@ -861,6 +862,7 @@ int validate_step(srq_model *m, int32_t sessions, srq_cache *const *caches, cons
         const srq_cache *c = caches[i];
         if (!c || c->released || c->p->m != m || std::find(seen.begin(), seen.end(), c) != seen.end())
             return fail(SRQ_EINVAL, "foreign, stale, released, or duplicate KV cache");
+        if (c->busy) return fail(SRQ_EINVAL, "KV cache is owned by a live decoder");
         seen.push_back(c);
         const int32_t len = lens[i];
         if (len < 1 || len > 1024 - n)
@@ -1334,6 +1336,7 @@ int srq_decoder_create(srq_exec *e, srq_model *m, srq_cache *c, int32_t first_to
     if (!e || !m || !c || !out) return fail(SRQ_EINVAL, "null pointer");
     *out = nullptr;
     if (c->released || c->p->m != m) return fail(SRQ_EINVAL, "foreign or released KV cache");
+    if (c->busy) return fail(SRQ_EINVAL, "KV cache is owned by a live decoder");
     if (first_token < 0 || first_token >= m->c.vocab) return fail(SRQ_EINVAL, "token outside vocabulary");
     if (max_steps < 1 || max_steps > m->c.context - c->pos) return fail(SRQ_ERANGE, "KV cache context exhausted");
     const int32_t end = c->pos + max_steps;
@@ -1350,6 +1353,7 @@ int srq_decoder_create(srq_exec *e, srq_model *m, srq_cache *c, int32_t first_to
     c->refs++;
     d->start_pos = c->pos;
     d->max_steps = max_steps;
+    c->busy = true;
     d->pt_stride = (m->c.context + kPageTokens - 1) / kPageTokens;
     while ((int32_t)c->pages.size() < pages) {
         c->pages.push_back(c->p->free_list.back());
@@ -1420,17 +1424,22 @@ int srq_decoder_run(srq_decoder *d, int32_t steps) {
     return SRQ_OK;
 }
 
-// Join, copy the tokens produced so far and commit the cache position.
+// Join, copy the tokens produced so far and commit the cache position.  A
+// step whose logits were not finite produced no token: the tokens before it
+// are returned with SRQ_ENONFINITE, and the position is committed through
+// that step (its KV row was written, as the reference's DecodeBatch commits
+// before inferHFIDs inspects the logits, M:1212-1238); later replays are
+// discarded.
 int srq_decoder_tokens(srq_decoder *d, int32_t *out, int32_t *count) {
     if (!d || !count) return fail(SRQ_EINVAL, "null pointer");
     DeviceGuard g(d->e->device);
     SRQ_HIP(hipStreamSynchronize(d->e->stream));
     int32_t err = 0;
     SRQ_HIP(hipMemcpy(&err, d->dbuf + 5, 4, hipMemcpyDeviceToHost));
-    if (out && d->steps)
-        SRQ_HIP(hipMemcpy(out, d->dbuf + 6 + d->pt_stride, (size_t)d->steps * 4, hipMemcpyDeviceToHost));
-    *count = d->steps;
-    d->c->pos = d->start_pos + d->steps;
+    const int32_t good = err > 0 ? std::min(err - 1, d->steps) : d->steps;
+    if (out && good) SRQ_HIP(hipMemcpy(out, d->dbuf + 6 + d->pt_stride, (size_t)good * 4, hipMemcpyDeviceToHost));
+    *count = good;
+    d->c->pos = d->start_pos + (err > 0 ? std::min(err, d->steps) : d->steps);
     if (err) return fail(SRQ_ENONFINITE, "non-finite HF logits");
     return SRQ_OK;
 }
@@ -1445,6 +1454,7 @@ int srq_decoder_destroy(srq_decoder *d) {
         if (d->dbuf) (void)hipFree(d->dbuf);
         d->ws.release_all();
     }
+    d->c->busy = false;
     cache_unref(d->c);
     model_unref(d->m);
     exec_unref(d->e);
@@ -1481,7 +1491,12 @@ int srq_generate_greedy(srq_exec *e, srq_model *m, srq_cache *c, const int32_t *
         rc = srq_decoder_run(d, k);
         int32_t got = 0;
         if (rc == SRQ_OK) rc = srq_decoder_tokens(d, out_tokens + 1, &got);
-        if (rc != SRQ_OK) break;
+        if (rc != SRQ_OK) {
+            // Non-finite logits: the tokens before that step stand (the
+            // reference returns them with the error, M:1212-1238).
+            if (rc == SRQ_ENONFINITE) *produced = 1 + got;
+            break;
+        }
         done = got;
         bool stop = false;
         if (eos >= 0)

@@ -439,16 +439,17 @@ __device__ __forceinline__ void merge_splits(const AttnArgs &A, const float *par
     float o[kMergePairs];
 #pragma unroll
     for (int k = 0; k < kMergePairs; ++k) o[k] = 0.0f;
-    // Few (head, dim) pairs and many splits (one head of a long-context
-    // decode row): groups of threads take parts of the split range, so no
-    // thread idles.  Up to kFusedSplits splits the order stays the fused
-    // kernel's (one FMA chain per pair).
-    // (GROUPS: the one-head combine; the many-head one never needs it.)
+    // Summation order of a (head, dim) pair, fixed by head_dim and the
+    // head's split count alone, so a row's output does not depend on the
+    // other rows of its step: up to kFusedSplits splits (and past
+    // kMergeChunk) one FMA chain over the splits in order, the fused
+    // kernel's order; in between, ng groups of consecutive splits, each
+    // summed from zero, then the group sums added in group order.
+    // GROUPS (the one-head combine of decode-sized batches): the groups run
+    // on separate threads, so none idles; otherwise one thread sums its
+    // pair's groups one after another, in the same order.
     __shared__ float gs[GROUPS ? 256 : 1];
-    const int pairs = nh * hd;
-    const int ng = GROUPS && pairs <= 128 && 256 % pairs == 0 && used > kFusedSplits && used <= kMergeChunk
-                       ? 256 / pairs
-                       : 1;
+    const int ng = hd <= 128 && 256 % hd == 0 && used > kFusedSplits && used <= kMergeChunk ? 256 / hd : 1;
     for (int c0 = 0; c0 < used; c0 += kMergeChunk) {
         const int cnt = min(kMergeChunk, used - c0);
         for (int t = tid; t < nh * cnt; t += 256) {
@@ -456,18 +457,18 @@ __device__ __forceinline__ void merge_splits(const AttnArgs &A, const float *par
             cf[g][i] = (float)exp((double)partial((float *)part, row, h0 + g, c0 + i, A.heads, nsplit, hd)[0] - lse[g]);
         }
         __syncthreads();
-        if (GROUPS && ng > 1) {
+        const int per = (cnt + ng - 1) / ng;
+        if (GROUPS && ng > 1 && nh == 1) {
             // Thread group q of ng sums splits [q*per, (q+1)*per) of its
             // (head, dim) pair; the groups' sums are added in group order.
-            const int pidx = tid % pairs, q = tid / pairs, per = (cnt + ng - 1) / ng;
-            const int g = pidx / hd, j = pidx - g * hd;
-            const float *pb = partial((float *)part, row, h0 + g, c0, A.heads, nsplit, hd) + 4 + j;
-            gs[tid] = merge_range(pb, hd, cf[g], q * per, min(cnt, q * per + per), 0.0f);
+            const int j = tid % hd, q = tid / hd;
+            const float *pb = partial((float *)part, row, h0, c0, A.heads, nsplit, hd) + 4 + j;
+            gs[tid] = merge_range(pb, hd, cf[0], q * per, min(cnt, q * per + per), 0.0f);
             __syncthreads();
             if (q == 0) {
-                float v = gs[pidx];
-                for (int r = 1; r < ng; ++r) v += gs[r * pairs + pidx];
-                A.out[(int64_t)row * A.heads * hd + (int64_t)(h0 + g) * hd + j] = v;
+                float v = gs[j];
+                for (int r = 1; r < ng; ++r) v += gs[r * hd + j];
+                A.out[(int64_t)row * A.heads * hd + (int64_t)h0 * hd + j] = v;
             }
             return;
         }
@@ -477,7 +478,13 @@ __device__ __forceinline__ void merge_splits(const AttnArgs &A, const float *par
             if (pidx >= nh * hd) break;
             const int g = pidx / hd, j = pidx - g * hd;
             const float *pb = partial((float *)part, row, h0 + g, c0, A.heads, nsplit, hd) + 4 + j;
-            o[k] = merge_range(pb, hd, cf[g], 0, cnt, o[k]);
+            if (ng > 1) {
+                float v = merge_range(pb, hd, cf[g], 0, min(cnt, per), 0.0f);
+                for (int q = 1; q < ng; ++q) v += merge_range(pb, hd, cf[g], q * per, min(cnt, q * per + per), 0.0f);
+                o[k] = v;
+            } else {
+                o[k] = merge_range(pb, hd, cf[g], 0, cnt, o[k]);
+            }
         }
         __syncthreads();
     }
@@ -654,6 +661,7 @@ __global__ __launch_bounds__(256) void attn_fused_kernel(const AttnArgs A, float
 // covers positions [i*split_len, (i+1)*split_len).  GROUPS (decode-sized
 // batches): thread groups share a head's split range; larger batches keep
 // the smaller register footprint, many workgroups being resident anyway.
+// Both give the same bits (merge_splits).
 template <bool GROUPS>
 __global__ __launch_bounds__(256) void attn_combine_kernel(const AttnArgs A, const float *__restrict__ part,
                                                            int nsplit, int split_len) {

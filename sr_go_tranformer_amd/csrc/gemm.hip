@@ -19,8 +19,8 @@
 //  - Split K: when the (features x rows) tiles alone cannot fill the chip
 //    (few rows per step, narrow outputs), blockIdx.z takes a slice of the
 //    K steps and writes its partial sums to scratch; gemm_reduce_kernel adds
-//    the slices in slice order, then the residual.  Results are
-//    deterministic for a given (n, rows, cols).
+//    the slices in slice order, then the residual.  The slice count depends
+//    on (rows, cols) only, so a row's bits do not depend on n.
 //  - Rows holding any |x| > f32(MaxFloat32/(2*64*127)) (M:4346-4354) are
 //    detected while staging x and recomputed in FP64 (linearQ8WideInto /
 //    linearQ4WideInto, M:4356-4382, M:4754-4780): by the workgroup itself
@@ -34,7 +34,6 @@ namespace {
 
 constexpr int BN = 128, BK = 32, LDK = BK + 4;
 constexpr int kCUs = 256;          // MI355X compute units
-constexpr int kFillWGs = 512;      // two resident workgroups on each CU
 constexpr int kMinSliceInputs = 256;  // inputs per split-K slice, at least
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
@@ -805,10 +804,18 @@ struct GemmPlan {
     int bm, tn, slices, kper;  // tn: 16-feature tiles per wave of the bf16 kernel
 };
 
-// Tile height from n.  With fewer tiles than CUs, K slices bring the grid
-// to kFillWGs workgroups (kCUs for 32-row tiles), each slice at least 256
-// inputs; from one tile per CU up, the slices' partial sums would cost more
-// than the idle CUs.
+// Tile height and width from n; K slices from the matrix shape alone.
+//
+// A row's result is fixed by the K slices (each slice's chain of block
+// sums, then the slices added in order); the tile height and width only
+// decide which workgroup computes it.  The slice count therefore depends on
+// (rows, cols) and never on n, so a row's bits are the same whatever other
+// rows share the call (batch invariance, q8_test.go:88-92).  It is the count
+// that fills the chip for one 32-row tile of outputs: with fewer feature
+// tiles than CUs, slices of at least 256 inputs bring the grid to one
+// workgroup per CU (each slice's partial sums cost as much traffic as a
+// share of the weights, which outweighs a second resident workgroup).
+// Larger n adds row tiles to the same slices.
 GemmPlan plan_gemm(int fmt, int32_t n, int64_t rows, int64_t cols) {
     GemmPlan p;
     p.x3 = (fmt == SRQ_Q8 || fmt == SRQ_Q4) && cols % kBlock == 0;
@@ -819,18 +826,13 @@ GemmPlan plan_gemm(int fmt, int32_t n, int64_t rows, int64_t cols) {
     // 3072 x 8192 24.9 -> 23.3 us, 5120 x 3072 20.0 -> 18.9 us; at 16384
     // rows the 256-feature tile stays ahead, 30.4 against 33.5 us).
     p.tn = p.bm == 32 && rows <= 8192 ? 2 : 4;
-    const int bn = p.x3 ? 64 * p.tn : BN, bk = p.x3 ? kBlock : BK;
-    const int64_t tiles = ((rows + bn - 1) / bn) * ((n + p.bm - 1) / p.bm);
+    const int bk = p.x3 ? kBlock : BK;
+    const int bn32 = p.x3 ? 64 * (rows <= 8192 ? 2 : 4) : BN;  // feature tile of a 32-row plan
+    const int64_t tiles = (rows + bn32 - 1) / bn32;
     const int ksteps = (int)(cols / bk), min_steps = kMinSliceInputs / bk;
     int slices = 1;
-    if (tiles < kCUs) {
-        // 32-row tiles (n <= 32) aim for one workgroup per CU: each slice's
-        // partial sums cost as much traffic as a share of the weights, which
-        // outweighs the second resident workgroup (Llama-3.2-3B batched
-        // steps: 4% faster; 256-row prefill GEMMs keep two per CU).
-        const int64_t fill = p.bm == 32 ? kCUs : kFillWGs, want = (fill + tiles - 1) / tiles;
-        slices = (int)std::max<int64_t>(1, std::min<int64_t>(want, ksteps / min_steps));
-    }
+    if (tiles < kCUs)
+        slices = (int)std::max<int64_t>(1, std::min<int64_t>((kCUs + tiles - 1) / tiles, ksteps / min_steps));
     p.kper = (ksteps + slices - 1) / slices;
     p.slices = (ksteps + p.kper - 1) / p.kper;
     return p;

@@ -200,8 +200,9 @@ __global__ __launch_bounds__(kArgThreads) void decode_tail_kernel(const DecodeTa
     const int tid = threadIdx.x;
     if (tid == 0) {
         A.token[0] = id;
-        if (bad) A.err[0] = 1;
         const int c = A.counter[0], p = A.pos[0] + 1;
+        // The first step with non-finite logits, as c + 1 (0: none yet).
+        if (bad && A.err[0] == 0) A.err[0] = c + 1;
         A.out[c] = id;
         A.counter[0] = c + 1;
         A.embed_id[0] = id;

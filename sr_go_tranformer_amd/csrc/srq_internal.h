@@ -156,7 +156,8 @@ int launch_argmax(hipStream_t s, const float *logits, int32_t rows, int32_t voca
 // Tail of a replayed greedy decode step (one row): argmax of `logits` ->
 // token; out[counter] = token, counter + 1, embed_id = token, pos + 1; then,
 // if counter < steps, x = the token's embedding row and the row plan
-// (kvoff[0], rope_cs[0..head_dim)) of the new position.
+// (kvoff[0], rope_cs[0..head_dim)) of the new position.  err[0] records
+// the first step whose logits held a non-finite value, as its counter + 1.
 struct DecodeTailArgs {
     const float *logits;
     int32_t vocab;

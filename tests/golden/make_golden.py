@@ -27,7 +27,8 @@ REF = "/root/reference/testdata"
 HERE = os.path.dirname(os.path.abspath(__file__))
 
 FIXTURES = ["hf-llama/f32", "hf-llama/f16", "hf-llama/bf16", "hf-llama/untied-f32", "hf-llama3/f32",
-            "hf-llama3/bf16", "hf-mistral/f32", "hf-mistral/bf16", "hf-qwen2/f32"]
+            "hf-llama3/f16", "hf-llama3/bf16", "hf-mistral/f32", "hf-mistral/f16", "hf-mistral/bf16",
+            "hf-qwen2/f32", "hf-qwen2/f16", "hf-qwen2/untied-bf16"]
 
 
 def read_safetensors(path):

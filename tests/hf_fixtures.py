@@ -7,8 +7,8 @@ import os
 import numpy as np
 
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
-NAMES = ["llama_f32", "llama_f16", "llama_bf16", "llama_untied-f32", "llama3_f32", "llama3_bf16",
-         "mistral_f32", "mistral_bf16", "qwen2_f32"]
+NAMES = ["llama_f32", "llama_f16", "llama_bf16", "llama_untied-f32", "llama3_f32", "llama3_f16", "llama3_bf16",
+         "mistral_f32", "mistral_f16", "mistral_bf16", "qwen2_f32", "qwen2_f16", "qwen2_untied-bf16"]
 MATRICES = ("q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj", "down_proj")
 
 

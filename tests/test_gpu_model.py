@@ -61,8 +61,8 @@ def test_fp32_step_matches_transformers(ex, name, chunk):
         absnear(v, fx.v[layer], 2e-5)
 
 
-@pytest.mark.parametrize("name", ["llama_f32", "llama_untied-f32", "llama3_f32", "mistral_f32", "qwen2_f32",
-                                  "mistral_bf16"])
+@pytest.mark.parametrize("name", ["llama_f32", "llama_untied-f32", "llama3_f32", "llama3_f16", "mistral_f32",
+                                  "mistral_f16", "mistral_bf16", "qwen2_f32", "qwen2_f16", "qwen2_untied-bf16"])
 @pytest.mark.parametrize("fmt", ["q8", "q4", "q4-mixed"])
 def test_quantized_step_matches_oracle(ex, name, fmt):
     print("quantized", name, fmt, flush=True)
@@ -219,6 +219,7 @@ def test_prefill_attention_tiles_match_oracle(ex, dim, heads, kv_heads):
     for layer in range(cfg.layers):
         k, v = ca.read(layer, 0, 660)
         near(k, np.stack([oa.row(layer, p, 0) for p in range(660)]))
+        near(v, np.stack([oa.row(layer, p, 1) for p in range(660)]))
 
 
 @pytest.mark.parametrize("dim,heads,kv_heads,fmt", [(512, 4, 1, "q8"), (1024, 8, 2, "q8"), (1024, 8, 2, "q4")])

@@ -60,7 +60,7 @@ def test_pack_bit_exact_edges(ex, cols, fmt):
 def test_pack_bit_exact_7b_shape(ex, fmt):
     print("pack 14336x4096", fmt, flush=True)
     rng = oracle.RNG(11)
-    m = rng.fill_normal(1024 * 4096, 0.02).reshape(1024, 4096)
+    m = rng.fill_normal(14336 * 4096, 0.02).reshape(14336, 4096)
     v, s = srq.pack(ex, m, fmt)
     ov, os_ = oracle.pack(m, oracle.Q8 if fmt == srq.Q8 else oracle.Q4)
     assert np.array_equal(s.view(np.uint32), os_.view(np.uint32))

@@ -59,7 +59,8 @@ def test_ragged_sessions(name):
     near(sel[1], fx.logits[3], 2e-5)
 
 
-@pytest.mark.parametrize("name", ["llama_f32", "llama_untied-f32", "llama3_f32", "mistral_f32", "qwen2_f32"])
+@pytest.mark.parametrize("name", ["llama_f32", "llama_untied-f32", "llama3_f32", "llama3_f16", "mistral_f32",
+                                  "mistral_f16", "qwen2_f32", "qwen2_f16", "qwen2_untied-bf16"])
 @pytest.mark.parametrize("fmt", ["q8", "q4", "q4-mixed"])
 def test_quantized_forward_equals_reconstructed_dense(name, fmt):
     fx = hf_fixtures.load(name)
