@@ -126,6 +126,20 @@ int srq_linear(srq_exec *e, float *y, const float *x, const srq_weight *w, int32
  * events).  Inputs must stay valid until the stream reaches the call. */
 int srq_linear_enqueue(srq_exec *e, float *y, const float *x, const srq_weight *w, int32_t n);
 
+/* No counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under HIP graph capture, serving loops that forbid
+ * hipMalloc): srq_linear_enqueue -- the same kernels and bit-identical
+ * results, stream-ordered on the executor without joining -- that allocates
+ * nothing.  The GEMM path's split-K partial sums and wide-row flags go to a
+ * fixed device array of SRQ_NOALLOC_SCRATCH_BYTES owned by the library (one
+ * per GPU, held until the process ends) instead of the executor's
+ * workspace; a call whose plan needs more is rejected with SRQ_EINVAL
+ * before anything is enqueued.  Every call on one GPU shares that array and
+ * leaves its contents behind: calls that overlap on one GPU (executors or
+ * streams not ordered against each other) race, so the caller orders them. */
+#define SRQ_NOALLOC_SCRATCH_BYTES (64u << 20)
+int srq_linear_noalloc(srq_exec *e, float *y, const float *x, const srq_weight *w, int32_t n);
+
 /* ---- model: HF Llama/Mistral/Qwen2 profile (M:4985-5050) --------------- */
 typedef struct {
     int32_t vocab, dim, layers, heads, kv_heads, hidden, context;

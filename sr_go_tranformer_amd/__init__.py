@@ -61,7 +61,8 @@ EXPORTS = [
     "srq_abi_version", "srq_last_error", "srq_device_count", "srq_alloc", "srq_free", "srq_copy_h2d",
     "srq_copy_d2h", "srq_copy_d2d", "srq_exec_create", "srq_exec_destroy", "srq_exec_synchronize",
     "srq_exec_stream", "srq_fill_normal", "srq_packed_bytes", "srq_pack", "srq_weight_create", "srq_weight_wrap",
-    "srq_weight_destroy", "srq_weight_info", "srq_dequant_rows", "srq_linear", "srq_linear_enqueue", "srq_model_create",
+    "srq_weight_destroy", "srq_weight_info", "srq_dequant_rows", "srq_linear", "srq_linear_enqueue",
+    "srq_linear_noalloc", "srq_model_create",
     "srq_model_load", "srq_model_destroy", "srq_model_resident_bytes", "srq_model_weight",
     "srq_model_rope_tables", "srq_model_load_safetensors", "srq_archive_check",
     "srq_pool_create", "srq_pool_destroy", "srq_cache_create", "srq_cache_destroy",
@@ -96,6 +97,7 @@ def _declare(L):
         "srq_dequant_rows": (C.c_int, [P, P, P, I32, P]),
         "srq_linear": (C.c_int, [P, P, P, P, I32]),
         "srq_linear_enqueue": (C.c_int, [P, P, P, P, I32]),
+        "srq_linear_noalloc": (C.c_int, [P, P, P, P, I32]),
         "srq_model_create": (C.c_int, [P, C.POINTER(ModelConfig), C.c_char_p, PP]),
         "srq_model_load": (C.c_int, [P, C.c_int, C.c_int, P, C.c_int]),
         "srq_model_destroy": (C.c_int, [P]),

@@ -18,6 +18,13 @@
 
 #include "srq_internal.h"
 
+// Scratch of srq_linear_noalloc (split-K partial sums and wide-row flags of
+// the GEMM path): a fixed array of the code object, one copy per GPU, held
+// until the process ends.  Host code never passes its name to a kernel (on
+// the host it is only a stand-in for the symbol): each device's address is
+// looked up once, when the device is prepared, and used from then on.
+static __device__ __align__(256) unsigned char scratch[SRQ_NOALLOC_SCRATCH_BYTES];
+
 namespace srq {
 
 static thread_local std::string g_err;
@@ -36,16 +43,28 @@ void clear_error() { g_err.clear(); }
 
 namespace {
 
+constexpr int kMaxDevices = 64;
 std::mutex g_prep_mu;
-std::vector<char> g_prepared;
+bool g_prepared[kMaxDevices];
+// Device address of `scratch` on each prepared device (written under
+// g_prep_mu before g_prepared is set; read only through an executor of that
+// device, which exists only after its preparation).
+void *g_noalloc_scratch[kMaxDevices];
 
+// Once per device, with that device current: kernel attributes, and the
+// device's address of the no-allocation scratch array.
 int prepare_device(int device) {
+    if (device < 0 || device >= kMaxDevices) return fail(SRQ_EINVAL, "device %d above the supported %d", device, kMaxDevices);
     std::lock_guard<std::mutex> lock(g_prep_mu);
-    if ((int)g_prepared.size() <= device) g_prepared.resize(device + 1, 0);
     if (g_prepared[device]) return SRQ_OK;
     SRQ_CHECK(gemv_prepare());
     SRQ_CHECK(attention_prepare());
-    g_prepared[device] = 1;
+    void *p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+        return fail(SRQ_EDEVICE, "no-allocation scratch lookup failed: %s", hipGetErrorString(e));
+    g_noalloc_scratch[device] = p;
+    g_prepared[device] = true;
     return SRQ_OK;
 }
 
@@ -289,13 +308,23 @@ constexpr int32_t kLinearGemmRows = 16;
 // 14% faster this way (Llama-3.2-3B shape, 32 sessions).
 constexpr int32_t kStepGemmRows = 8;
 
+// Device scratch the GEMM of y = x . W^T needs for n rows (split-K partial
+// sums and wide-row flags); 0 on the GEMV path.
+size_t linear_scratch_bytes(const srq_weight &w, int32_t n, int32_t gemm_rows = kLinearGemmRows) {
+    return n > gemm_rows && gemm_ok(w.fmt, w.cols) ? gemm_scratch_bytes(w.fmt, n, w.rows, w.cols) : 0;
+}
+
 // y[n x w.rows] = x . W^T for n rows through the GEMV (chunks of 8) or the
 // MFMA GEMM (n > gemm_rows, K multiple of 32), with optional fused RMSNorm.
+// fixed (non-null): the GEMM's scratch is that caller-provided buffer of
+// fixed_bytes instead of the workspace, which then never grows.
 int run_linear(srq_exec *e, Workspace &ws, const srq_weight &w, const float *x, int32_t n, float *y, int64_t y_stride,
-               const float *norm_w, double eps, const float *residual, int32_t gemm_rows = kLinearGemmRows) {
+               const float *norm_w, double eps, const float *residual, int32_t gemm_rows = kLinearGemmRows,
+               void *fixed = nullptr, size_t fixed_bytes = 0) {
     if (n > gemm_rows && gemm_ok(w.fmt, w.cols) && !norm_w) {
-        SRQ_CHECK(ensure(ws.flags, gemm_scratch_bytes(w.fmt, n, w.rows, w.cols), e->stream));
         GemmArgs g{w.fmt, w.values, w.scales, w.rows, w.cols, x, n, y, y_stride, residual, nullptr};
+        if (fixed) return launch_gemm(e->stream, g, fixed, fixed_bytes);
+        SRQ_CHECK(ensure(ws.flags, gemm_scratch_bytes(w.fmt, n, w.rows, w.cols), e->stream));
         return launch_gemm(e->stream, g, ws.flags.p, ws.flags.n);
     }
     const int nb = gemv_max_rows(w.fmt, w.cols, norm_w != nullptr, 0);
@@ -545,6 +574,27 @@ int srq_linear_enqueue(srq_exec *e, float *y, const float *x, const srq_weight *
         return fail(SRQ_EINVAL, "y overlaps x");
     DeviceGuard g(e->device);
     return run_linear(e, e->ws, *w, x, n, y, w->rows, nullptr, 0.0, nullptr);
+}
+
+// srq_linear_enqueue with the split-K scratch in the library's fixed device
+// array: no allocation of any kind (no executor workspace growth).
+int srq_linear_noalloc(srq_exec *e, float *y, const float *x, const srq_weight *w, int32_t n) {
+    if (!e || !y || !x || !w) return fail(SRQ_EINVAL, "null pointer");
+    if (n < 1 || n > 1024) return fail(SRQ_EINVAL, "linear rows n=%d outside 1..1024", n);
+    const char *yb = (const char *)y, *xb = (const char *)x;
+    if (yb < xb + (size_t)n * w->cols * 4 && xb < yb + (size_t)n * w->rows * 4)
+        return fail(SRQ_EINVAL, "y overlaps x");
+    const size_t need = linear_scratch_bytes(*w, n);
+    if (need > (size_t)SRQ_NOALLOC_SCRATCH_BYTES)
+        return fail(SRQ_EINVAL,
+                    "srq_linear_noalloc: %d rows of a %lld x %lld matrix need %zu bytes of scratch, above the "
+                    "fixed %zu (use srq_linear)",
+                    n, (long long)w->rows, (long long)w->cols, need, (size_t)SRQ_NOALLOC_SCRATCH_BYTES);
+    void *buf = g_noalloc_scratch[e->device];  // set when e's device was prepared
+    if (!buf) return fail(SRQ_EDEVICE, "no-allocation scratch missing on device %d", e->device);
+    DeviceGuard g(e->device);
+    return run_linear(e, e->ws, *w, x, n, y, w->rows, nullptr, 0.0, nullptr, kLinearGemmRows, buf,
+                      (size_t)SRQ_NOALLOC_SCRATCH_BYTES);
 }
 
 // ------------------------------------------------------------------- model
