@@ -521,13 +521,18 @@ __device__ __forceinline__ Unit unit_rows(const GemvArgs &A, int u) {
     return t;
 }
 
+// EPI_RESID with RS: a wave stages the residual values of at most this many
+// units (its share of the rows) before its weight prefetch.
+constexpr int kResidUnits = 16;
+
 // Dynamic LDS of the streaming kernel, in floats: x rows [NB x ld], then the
 // RMSNorm weight [ld] (NORM), then per batch row its RoPE {cos, sin} pairs
-// [NB x head_dim] and the q/k/v bias [rows] (EPI_ROPE_KV).
+// [NB x head_dim] and the q/k/v bias [rows] (EPI_ROPE_KV), then with RS per
+// wave the residual values of its units [kResidUnits x NB].
 struct StreamLds {
-    int ld, x, norm, rope, bias, total;
+    int ld, x, norm, rope, bias, rs, total;
 };
-template <int NB, int EPI, bool NORM>
+template <int NB, int EPI, bool NORM, bool RS>
 __host__ __device__ __forceinline__ StreamLds stream_lds(const GemvArgs &A, int ld) {
     StreamLds L;
     L.ld = ld;
@@ -536,17 +541,40 @@ __host__ __device__ __forceinline__ StreamLds stream_lds(const GemvArgs &A, int 
     L.rope = L.norm + (NORM ? ld : 0);
     L.bias = L.rope + (EPI == EPI_ROPE_KV ? NB * A.head_dim : 0);
     const int bias_n = EPI == EPI_ROPE_KV && A.bias ? (int)A.rows : 0;
-    L.total = L.bias + ((bias_n + 3) & ~3);
+    L.rs = L.bias + ((bias_n + 3) & ~3);
+    L.total = L.rs + (RS ? kStreamWaves * kResidUnits * NB : 0);
     return L;
 }
 
 struct StreamSmem {
-    double ss[8][kStreamWaves];
-    float a[8];
-    int wide[8];
-    int any_wide;
+    double ss[8][kStreamWaves];  // per batch row and wave: f64 sum of squares (RMSNorm)
+    int wflag[kStreamWaves];     // per wave: bit b set if a |x| of batch row b exceeds kWideLimit
     int64_t kvoff[8];  // EPI_ROPE_KV: element offset of each batch row's K row (layer 0)
 };
+
+// EPI_ROPE_KV: each batch row's KV offset and its position's {cos, sin}
+// pairs, loaded into registers ahead of the weight prefetch (loads complete
+// in issue order, so loading them after it would make staging wait for the
+// whole prefetch) and stored to LDS while staging.
+template <int NB, int EPI>
+struct RopeStage {
+    static constexpr int K = EPI == EPI_ROPE_KV ? (NB * 256 + kStreamThreads - 1) / kStreamThreads : 0;  // head_dim <= 256
+    float cs[K > 0 ? K : 1];
+    int64_t kv;
+};
+
+template <int NB, int EPI>
+__device__ __forceinline__ void rope_stage_load(const GemvArgs &A, RopeStage<NB, EPI> &r) {
+    if constexpr (EPI == EPI_ROPE_KV) {
+        const int tid = threadIdx.x, hd = A.head_dim;
+        r.kv = tid < NB && tid < A.n ? A.meta.kvoff[A.row0 + tid] : 0;
+#pragma unroll
+        for (int k = 0; k < RopeStage<NB, EPI>::K; ++k) {
+            const int i = tid + k * kStreamThreads, b = i / hd;
+            r.cs[k] = i < NB * hd && b < A.n ? A.meta.rope_cs[(int64_t)(A.row0 + b) * hd + (i - b * hd)] : 0.0f;
+        }
+    }
+}
 
 // Stage the n activation rows of x into LDS (permuted, zero past cols), the
 // norm weight, RoPE rows, KV offsets and bias; apply the fused RMSNorm
@@ -594,20 +622,19 @@ __device__ __forceinline__ void stage_pass_load(const GemvArgs &A, int c0, Stage
 }
 
 template <int E, int CW, int NB, int EPI, bool NORM>
-__device__ __forceinline__ void stage_stream(const GemvArgs &A, float *lds, const StreamLds &L, StreamSmem &sm,
-                                             bool vec, StagePass<NB, NORM> &sp) {
+__device__ __forceinline__ int stage_stream(const GemvArgs &A, float *lds, const StreamLds &L, StreamSmem &sm,
+                                            bool vec, StagePass<NB, NORM> &sp, const RopeStage<NB, EPI> &rs) {
     constexpr int NT = kStreamThreads, NW = kStreamWaves;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int cols = (int)A.cols, ld = L.ld;
     float *xs = lds + L.x, *wn = lds + L.norm;
-    if (tid < NB) sm.wide[tid] = 0;
-    if (tid == 0) sm.any_wide = 0;
     if constexpr (EPI == EPI_ROPE_KV) {
-        if (tid < NB) sm.kvoff[tid] = tid < A.n ? A.meta.kvoff[A.row0 + tid] : 0;
+        if (tid < NB) sm.kvoff[tid] = rs.kv;
         const int hd = A.head_dim;
-        for (int i = tid; i < NB * hd; i += NT) {
-            const int b = i / hd;
-            lds[L.rope + i] = b < A.n ? A.meta.rope_cs[(int64_t)(A.row0 + b) * hd + (i - b * hd)] : 0.0f;
+#pragma unroll
+        for (int k = 0; k < RopeStage<NB, EPI>::K; ++k) {
+            const int i = tid + k * NT;
+            if (i < NB * hd) lds[L.rope + i] = rs.cs[k];
         }
         if (A.bias)
             for (int i = tid; i < (int)A.rows; i += NT) lds[L.bias + i] = A.bias[i];
@@ -615,6 +642,11 @@ __device__ __forceinline__ void stage_stream(const GemvArgs &A, float *lds, cons
     double ss[NB];
 #pragma unroll
     for (int b = 0; b < NB; ++b) ss[b] = 0.0;
+    int wide = 0;  // bit b: |x| > kWideLimit in a column of batch row b this thread staged
+    auto flag4 = [](const float4 v) {
+        return (int)(fabsf(v.x) > kWideLimit) | (int)(fabsf(v.y) > kWideLimit) | (int)(fabsf(v.z) > kWideLimit) |
+               (int)(fabsf(v.w) > kWideLimit);
+    };
     if (vec) {
         // The first pass (c0 = tid * 4) is already in sp.
         constexpr int U = StagePass<NB, NORM>::U;
@@ -633,6 +665,8 @@ __device__ __forceinline__ void stage_stream(const GemvArgs &A, float *lds, cons
                     if (NORM)
                         ss[b] += (double)t[b][u].x * t[b][u].x + (double)t[b][u].y * t[b][u].y +
                                  (double)t[b][u].z * t[b][u].z + (double)t[b][u].w * t[b][u].w;
+                    else
+                        wide |= flag4(t[b][u]) << b;
                 }
                 if (NORM) *(float4 *)(wn + i) = w[u];
             }
@@ -645,6 +679,7 @@ __device__ __forceinline__ void stage_stream(const GemvArgs &A, float *lds, cons
                 const float v = (b < A.n && c < cols) ? A.x[(int64_t)b * cols + c] : 0.0f;
                 xs[b * ld + i] = v;
                 ss[b] += (double)v * (double)v;
+                wide |= (int)(fabsf(v) > kWideLimit) << b;
             }
             if (NORM) wn[i] = c < cols ? A.norm_w[c] : 0.0f;
         }
@@ -655,42 +690,51 @@ __device__ __forceinline__ void stage_stream(const GemvArgs &A, float *lds, cons
             const double t = wave_sum_d(ss[b]);
             if (lane == 0) sm.ss[b][wave] = t;
         }
-    }
-    lds_barrier();
-    if (NORM) {
-        if (tid < NB) {
-            double t = 0.0;
-            for (int w = 0; w < NW; ++w) t += sm.ss[tid][w];
-            sm.a[tid] = (float)(1.0 / sqrt(t / (double)cols + A.norm_eps));
-        }
         lds_barrier();
-    }
-    // LDS only: normalise ((x*a)*w, unfused) and flag wide rows.  cols is a
-    // multiple of 4 for every streaming layout.
+        // Every thread forms a = f32(1/sqrt(Sum f64(x^2)/d + eps)) from the
+        // waves' sums (the same order everywhere, so the same bits), then
+        // normalises ((x*a)*w, unfused) the columns it staged itself -- its
+        // own LDS writes, so no barrier is needed before reading them -- and
+        // flags wide rows.
+        wide = 0;
 #pragma unroll
-    for (int b = 0; b < NB; ++b) {
-        const float a = NORM ? sm.a[b] : 1.0f;
-        int wide = 0;
-        for (int c = tid * 4; c < cols; c += NT * 4) {
-            const int i = xidx<E, CW>(c);
-            float4 v = *(float4 *)(xs + b * ld + i);
-            if (NORM) {
-                const float4 w = *(const float4 *)(wn + i);
-                v.x = __fmul_rn(__fmul_rn(v.x, a), w.x);
-                v.y = __fmul_rn(__fmul_rn(v.y, a), w.y);
-                v.z = __fmul_rn(__fmul_rn(v.z, a), w.z);
-                v.w = __fmul_rn(__fmul_rn(v.w, a), w.w);
-                *(float4 *)(xs + b * ld + i) = v;
+        for (int b = 0; b < NB; ++b) {
+            double t = 0.0;
+            for (int w = 0; w < NW; ++w) t += sm.ss[b][w];
+            const float a = (float)(1.0 / sqrt(t / (double)cols + A.norm_eps));
+            if (vec) {
+                for (int c = tid * 4; c < cols; c += NT * 4) {
+                    const int i = xidx<E, CW>(c);
+                    float4 v = *(float4 *)(xs + b * ld + i);
+                    const float4 w = *(const float4 *)(wn + i);
+                    v.x = __fmul_rn(__fmul_rn(v.x, a), w.x);
+                    v.y = __fmul_rn(__fmul_rn(v.y, a), w.y);
+                    v.z = __fmul_rn(__fmul_rn(v.z, a), w.z);
+                    v.w = __fmul_rn(__fmul_rn(v.w, a), w.w);
+                    *(float4 *)(xs + b * ld + i) = v;
+                    wide |= flag4(v) << b;
+                }
+            } else {
+                for (int c = tid; c < cols; c += NT) {
+                    const int i = xidx<E, CW>(c);
+                    const float v = __fmul_rn(__fmul_rn(xs[b * ld + i], a), wn[i]);
+                    xs[b * ld + i] = v;
+                    wide |= (int)(fabsf(v) > kWideLimit) << b;
+                }
             }
-            wide |= (int)(fabsf(v.x) > kWideLimit) | (int)(fabsf(v.y) > kWideLimit) |
-                    (int)(fabsf(v.z) > kWideLimit) | (int)(fabsf(v.w) > kWideLimit);
-        }
-        if (wide && b < A.n) {
-            sm.wide[b] = 1;
-            sm.any_wide = 1;
         }
     }
+    // One flag word per wave (an OR over its lanes), then every thread ORs
+    // the waves' words after the barrier: the workgroup-uniform mask of
+    // batch rows that take the FP64 pass.
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) wide |= __shfl_xor(wide, o, 64);
+    if (lane == 0) sm.wflag[wave] = wide;
     lds_barrier();
+    int mask = 0;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) mask |= sm.wflag[w];
+    return mask & ((1 << A.n) - 1);
 }
 
 // Write one unit's results: lane b (b < NB, b < n, write) stores batch
@@ -758,12 +802,27 @@ __device__ __forceinline__ void unit_epilogue(const GemvArgs &A, const Unit &t, 
     }
 }
 
-template <int FMT, int NB, int EPI, bool NORM, bool WMAJOR>
+// G: chunks that share one load of block scales.  A step's lane needs the
+// scale of its 64-column block; one dword load per lane covers 64
+// consecutive scales, which are the blocks of G chunks (Q8: 4 x 16, Q4:
+// 2 x 32).  With G > 1 the load is issued only at the first step of each
+// group of G chunks -- a fixed slot of the unrolled prefetch ring, since
+// every row holds a whole number of groups -- and each step takes its lane's
+// scale from the group's register by a cross-lane permute.  A load per step
+// instead (G = 1) doubles the vector memory instructions of the stream:
+// 23.2 us against 22.3 us for the 28672 x 4096 GEMV.
+//
+// RS (EPI_RESID, at most kResidUnits units per wave): the residual values of
+// the wave's units are loaded once, ahead of the prefetch, and kept in LDS,
+// instead of one residual load per step riding in the weight stream.
+template <int FMT, int NB, int EPI, bool NORM, bool WMAJOR, int G, bool RS>
 __global__ __launch_bounds__(kStreamThreads) void gemv_stream_kernel(const GemvArgs A) {
     using Ly = Lay<FMT, true>;
     constexpr int E = Ly::E, CW = Ly::CW, R = unit_rows_of<EPI>();
     // 8 row loads in flight per lane (two waves per SIMD, eight per CU).
     constexpr int P = 8 / R;
+    static_assert(P % G == 0 && (G == 1 || (WMAJOR && FMT != SRQ_F32)), "scale groups fill the prefetch ring");
+    static_assert(!RS || EPI == EPI_RESID, "staged residuals belong to the residual epilogue");
     extern __shared__ __attribute__((aligned(16))) float lds[];  // 16 B: ds_read_b128
     __shared__ StreamSmem sm;
     // The wave index is uniform: make it scalar so the step loop and its
@@ -771,7 +830,7 @@ __global__ __launch_bounds__(kStreamThreads) void gemv_stream_kernel(const GemvA
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int64_t cols = A.cols;
     const int nch = (int)((cols + CW - 1) / CW);
-    const StreamLds L = stream_lds<NB, EPI, NORM>(A, nch * CW);
+    const StreamLds L = stream_lds<NB, EPI, NORM, RS>(A, nch * CW);
     const int ld = L.ld;
     float *xs = lds + L.x;
 
@@ -822,19 +881,25 @@ __global__ __launch_bounds__(kStreamThreads) void gemv_stream_kernel(const GemvA
     uint4 wb[P][R];
     float sb[P][R];
     float eb[P];  // EPI_RESID: the unit's residual value, carried with each step
-    auto load_next = [&](uint4(&w)[R], float(&sc)[R], float &e) {
+    // group_start: constant once the ring is unrolled (slot % G == 0).
+    auto load_next = [&](uint4(&w)[R], float(&sc)[R], float &e, const bool group_start) {
         const bool ok = (int64_t)lch * CW + (int64_t)lane * E < cols;
         const int boff = ok ? lch * 1024 + lane * 16 : 0;
-        const int soff = ok ? lch * SPC + lane_sc : 0;
+        // G > 1: lane l loads scale l of the group (l mod G*SPC: Q8 with
+        // G = 2 needs 32), in bounds since rows are whole groups of chunks.
+        // The group is the one holding lch: a cursor parked on a wave's last
+        // step (any chunk of the row) still reads inside its row.
+        const int soff = G == 1 ? (ok ? lch * SPC + lane_sc : 0) : (lch & ~(G - 1)) * SPC + (lane & (G * SPC - 1));
 #pragma unroll
         for (int i = 0; i < R; ++i) {
             w[i] = ld_stream16(lw[i] + boff);
-            if constexpr (FMT != SRQ_F32)
-                sc[i] = ls[i][soff];
-            else
+            if constexpr (FMT != SRQ_F32) {
+                if (group_start) sc[i] = ls[i][soff];
+            } else {
                 sc[i] = 1.0f;
+            }
         }
-        if constexpr (EPI == EPI_RESID) e = *lres;
+        if constexpr (EPI == EPI_RESID && !RS) e = *lres;
         if (lch + 1 < nch) {
             ++lch;
         } else if (lu < ulast) {
@@ -843,24 +908,47 @@ __global__ __launch_bounds__(kStreamThreads) void gemv_stream_kernel(const GemvA
             set_rows(lu);
         }
     };
-    // The first staging pass is issued first; the weight prefetch, which
-    // does not depend on x, follows and streams through the staging.
+    // The first staging pass (and the q/k/v launch's RoPE rows and KV
+    // offsets) is issued first; the weight prefetch, which does not depend
+    // on x, follows and streams through the staging.
     const bool svec = stage_vec<NORM>(A);
     StagePass<NB, NORM> sp;
+    RopeStage<NB, EPI> rs;
     if (svec) stage_pass_load<NB, NORM>(A, tid * 4, sp);
+    rope_stage_load<NB, EPI>(A, rs);
+    // RS: lane b (< n) loads batch row b's residual of each of the wave's
+    // units (the host guarantees at most kResidUnits of them).
+    constexpr int NR = RS ? kResidUnits : 1;
+    float rsr[NR];
+    if constexpr (RS) {
+#pragma unroll
+        for (int j = 0; j < NR; ++j) {
+            rsr[j] = 0.0f;
+            if (j < myunits && lane < NB && lane < A.n)
+                rsr[j] = A.residual[(int64_t)lane * A.y_stride + unit_rows<EPI>(A, wid + j * nwaves).r[0]];
+        }
+    }
     // Every wave issues the prefetch, so it is straight-line code and the
     // compiler waits for the staging loads alone; a wave with no unit
     // re-reads unit 0's first chunks and discards them.
     set_rows(steps > 0 ? wid : 0);
 #pragma unroll
-    for (int p = 0; p < P; ++p) load_next(wb[p], sb[p], eb[p]);
-    stage_stream<E, CW, NB, EPI, NORM>(A, lds, L, sm, svec, sp);
+    for (int p = 0; p < P; ++p) load_next(wb[p], sb[p], eb[p], p % G == 0);
+    const int wmask = stage_stream<E, CW, NB, EPI, NORM>(A, lds, L, sm, svec, sp, rs);
     if (steps == 0) {  // wave-uniform; no barrier follows
         __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): no load outlives the wave
         return;
     }
+    // This wave's slice of the staged residuals, written and read by this
+    // wave only (its LDS operations complete in order): no barrier.
+    float *rsl = lds + L.rs + wave * (kResidUnits * NB);
+    if constexpr (RS) {
+#pragma unroll
+        for (int j = 0; j < NR; ++j)
+            if (j < myunits && lane < NB) rsl[j * NB + lane] = rsr[j];
+    }
     // Batch rows flagged wide are written by the FP64 pass below instead.
-    const bool fast_row = !(lane < NB && sm.wide[lane]);
+    const bool fast_row = !(lane < NB && ((wmask >> lane) & 1));
 
     float acc[R][NB];
 #pragma unroll
@@ -869,11 +957,25 @@ __global__ __launch_bounds__(kStreamThreads) void gemv_stream_kernel(const GemvA
         for (int b = 0; b < NB; ++b) acc[i][b] = 0.0f;
 
     int cu = wid;  // compute cursor
+    int kk = 0;    // its unit's index among the wave's units
     int ch = 0;
+    float sg[R];  // G > 1: the scales of the current group, kept past the refill of its slot
+#pragma unroll
+    for (int i = 0; i < R; ++i) sg[i] = 0.0f;
     for (int base = 0; base < steps; base += P) {
 #pragma unroll
         for (int k = 0; k < P; ++k) {
             const bool live = base + k < steps;  // wave-uniform
+            float scale[R];
+#pragma unroll
+            for (int i = 0; i < R; ++i) {
+                if constexpr (G == 1) {
+                    scale[i] = sb[k][i];
+                } else {
+                    if (k % G == 0) sg[i] = sb[k][i];
+                    scale[i] = __shfl(sg[i], (k % G) * SPC + lane_sc, 64);
+                }
+            }
             if (live) {
                 float wv[R][E];
 #pragma unroll
@@ -893,18 +995,20 @@ __global__ __launch_bounds__(kStreamThreads) void gemv_stream_kernel(const GemvA
 #pragma unroll
                         for (int e = 0; e < E; ++e) p = __builtin_fmaf(xv[e], wv[i][e], p);
                         if constexpr (FMT == SRQ_Q4) p *= 0.0625f;  // exact: undo the *16 decode
-                        acc[i][b] = __builtin_fmaf(p, sb[k][i], acc[i][b]);
+                        acc[i][b] = __builtin_fmaf(p, scale[i], acc[i][b]);
                     }
                 }
             }
-            const float resid = eb[k];  // this step's residual, before the slot is refilled
-            load_next(wb[k], sb[k], eb[k]);
+            // this step's residual (RS: the unit's staged value), read before the slot is refilled
+            const float resid = RS ? (lane < NB ? rsl[kk * NB + lane] : 0.0f) : eb[k];
+            load_next(wb[k], sb[k], eb[k], k % G == 0);
             if (!live) continue;
             const bool done = ch == nch - 1;
             const int udone = cu;
             if (done) {
                 ch = 0;
                 cu += nwaves;
+                ++kk;
             } else {
                 ++ch;
             }
@@ -926,12 +1030,12 @@ __global__ __launch_bounds__(kStreamThreads) void gemv_stream_kernel(const GemvA
 
     // FP64 pass for batch rows holding |x| > kWideLimit (M:4356-4382):
     // Sum_g f64(scale_g) * Sum_j f64(x_j) * f64(w_j), then the epilogue.
-    if (!sm.any_wide) return;
+    if (!wmask) return;
     for (int u = wid; u < U; u += nwaves) {
         const Unit t = unit_rows<EPI>(A, u);
         float v[R][NB] = {};
         for (int b = 0; b < NB; ++b) {
-            if (!sm.wide[b]) continue;
+            if (!((wmask >> b) & 1)) continue;
 #pragma unroll
             for (int i = 0; i < R; ++i) {
                 const uint8_t *wr = W + (int64_t)t.r[i] * rb;
@@ -979,6 +1083,31 @@ int gemv_wg_per_cu() {
 
 constexpr size_t kMaxLds = 150 * 1024;
 
+// The streaming kernel variant for a row layout: wave-major dealing for rows
+// of whole 1 KiB chunks, with as many chunks per scale load as divide the row
+// (Q8 4 or 2, Q4 2; a chunk holds 16 or 32 blocks).
+template <int FMT, int NB, int EPI, bool NORM, bool RS>
+int launch_grid(hipStream_t s, const GemvArgs &a, int nch, int64_t blocks) {
+    const size_t lds = (size_t)stream_lds<NB, EPI, NORM, RS>(a, nch * Lay<FMT, true>::CW).total * sizeof(float);
+    if (lds > kMaxLds)
+        return fail(SRQ_EINVAL, "gemv: activation rows do not fit LDS (n=%d cols=%lld)", NB, (long long)a.cols);
+    const dim3 grid((unsigned)blocks);
+    if (row_bytes(FMT, a.cols) % 1024 != 0) {
+        gemv_stream_kernel<FMT, NB, EPI, NORM, false, 1, RS><<<grid, kStreamThreads, lds, s>>>(a);
+    } else if constexpr (FMT == SRQ_F32) {
+        gemv_stream_kernel<FMT, NB, EPI, NORM, true, 1, RS><<<grid, kStreamThreads, lds, s>>>(a);
+    } else {
+        if (FMT == SRQ_Q8 && nch % 4 == 0)
+            gemv_stream_kernel<FMT, NB, EPI, NORM, true, (FMT == SRQ_Q8 ? 4 : 2), RS><<<grid, kStreamThreads, lds, s>>>(a);
+        else if (nch % 2 == 0)
+            gemv_stream_kernel<FMT, NB, EPI, NORM, true, 2, RS><<<grid, kStreamThreads, lds, s>>>(a);
+        else
+            gemv_stream_kernel<FMT, NB, EPI, NORM, true, 1, RS><<<grid, kStreamThreads, lds, s>>>(a);
+    }
+    SRQ_HIP(hipGetLastError());
+    return SRQ_OK;
+}
+
 template <int FMT, bool FAST, int NB, int EPI, bool NORM>
 int launch_t(hipStream_t s, const GemvArgs &a) {
     using Ly = Lay<FMT, FAST>;
@@ -987,9 +1116,8 @@ int launch_t(hipStream_t s, const GemvArgs &a) {
         // The kernel indexes rows, units and steps in 32 bits.
         if (a.rows >= (1LL << 30))
             return fail(SRQ_EINVAL, "gemv: %lld rows exceed the 2^30 row limit", (long long)a.rows);
-        const size_t lds = (size_t)stream_lds<NB, EPI, NORM>(a, nch * Ly::CW).total * sizeof(float);
-        if (lds > kMaxLds)
-            return fail(SRQ_EINVAL, "gemv: activation rows do not fit LDS (n=%d cols=%lld)", NB, (long long)a.cols);
+        if (EPI == EPI_ROPE_KV && (a.head_dim < 2 || a.head_dim > 256))
+            return fail(SRQ_EINVAL, "gemv: head_dim %d outside 2..256", a.head_dim);
         const int64_t units = unit_count<EPI>(a);
         int64_t blocks = (units + kStreamWaves - 1) / kStreamWaves;
         const int64_t cap = (int64_t)device_cus() * gemv_wg_per_cu();
@@ -998,12 +1126,14 @@ int launch_t(hipStream_t s, const GemvArgs &a) {
         if ((units / (blocks * kStreamWaves) + 1) * nch >= (1LL << 31))
             return fail(SRQ_EINVAL, "gemv: %lld x %lld exceeds the per-wave step limit", (long long)a.rows,
                         (long long)a.cols);
-        if (row_bytes(FMT, a.cols) % 1024 == 0)
-            gemv_stream_kernel<FMT, NB, EPI, NORM, true><<<(unsigned)blocks, kStreamThreads, lds, s>>>(a);
-        else
-            gemv_stream_kernel<FMT, NB, EPI, NORM, false><<<(unsigned)blocks, kStreamThreads, lds, s>>>(a);
-        SRQ_HIP(hipGetLastError());
-        return SRQ_OK;
+        // Residuals staged when every wave has at most kResidUnits units and
+        // their LDS slice fits.
+        if constexpr (EPI == EPI_RESID) {
+            const bool rs = (units + blocks * kStreamWaves - 1) / (blocks * kStreamWaves) <= kResidUnits &&
+                            (size_t)stream_lds<NB, EPI, NORM, true>(a, nch * Ly::CW).total * sizeof(float) <= kMaxLds;
+            if (rs) return launch_grid<FMT, NB, EPI, NORM, true>(s, a, nch, blocks);
+        }
+        return launch_grid<FMT, NB, EPI, NORM, false>(s, a, nch, blocks);
     } else {
         const size_t lds = (size_t)NB * nch * Ly::CW * sizeof(float);
         if (lds > kMaxLds)
@@ -1046,11 +1176,26 @@ hipError_t prepare_one() {
         return hipSuccess;
     } else {
         if constexpr (FAST) {
-            const hipError_t e = hipFuncSetAttribute((const void *)gemv_stream_kernel<FMT, NB, EPI, NORM, true>,
-                                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMaxLds);
-            if (e != hipSuccess) return e;
-            return hipFuncSetAttribute((const void *)gemv_stream_kernel<FMT, NB, EPI, NORM, false>,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMaxLds);
+            const void *k[8] = {(const void *)gemv_stream_kernel<FMT, NB, EPI, NORM, false, 1, false>,
+                                (const void *)gemv_stream_kernel<FMT, NB, EPI, NORM, true, 1, false>};
+            if constexpr (FMT != SRQ_F32) {
+                k[2] = (const void *)gemv_stream_kernel<FMT, NB, EPI, NORM, true, 2, false>;
+                k[3] = (const void *)gemv_stream_kernel<FMT, NB, EPI, NORM, true, (FMT == SRQ_Q8 ? 4 : 2), false>;
+            }
+            if constexpr (EPI == EPI_RESID) {
+                k[4] = (const void *)gemv_stream_kernel<FMT, NB, EPI, NORM, false, 1, true>;
+                k[5] = (const void *)gemv_stream_kernel<FMT, NB, EPI, NORM, true, 1, true>;
+                if constexpr (FMT != SRQ_F32) {
+                    k[6] = (const void *)gemv_stream_kernel<FMT, NB, EPI, NORM, true, 2, true>;
+                    k[7] = (const void *)gemv_stream_kernel<FMT, NB, EPI, NORM, true, (FMT == SRQ_Q8 ? 4 : 2), true>;
+                }
+            }
+            for (const void *f : k) {
+                if (!f) continue;
+                const hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMaxLds);
+                if (e != hipSuccess) return e;
+            }
+            return hipSuccess;
         } else {
             return hipFuncSetAttribute((const void *)gemv_kernel<FMT, false, NB, EPI, NORM>,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMaxLds);
