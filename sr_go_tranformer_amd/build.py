@@ -14,7 +14,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OBJ = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libsrq.so")
-SOURCES = ["pack.hip", "gemv.hip", "gemm.hip", "glue.hip", "attention.hip", "sample.hip", "api.cpp", "safetensors.cpp"]
+SOURCES = ["pack.hip", "gemv.hip", "gemv_q8.hip", "gemv_q4.hip", "gemv_f32.hip", "gemm.hip", "glue.hip", "attention.hip", "sample.hip", "api.cpp", "safetensors.cpp"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
