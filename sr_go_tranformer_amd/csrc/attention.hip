@@ -12,12 +12,15 @@
 // Split over positions (flash-decoding): workgroup (row, kv head, split)
 // scores kSplit positions for all query heads of its GQA group, so each K/V
 // row is read once per group.  It keeps the split's max m_i, FP64 sum
-// l_i = sum exp(score - m_i) and o_i = sum f32(exp(score - m_i)) v_s.  The
-// combine kernel forms lse = M + log(sum_i l_i exp(m_i - M)) and
-// out = sum_i f32(exp(m_i - lse)) o_i, which equals the reference's
+// l_i = sum exp(score - m_i) and o_i = sum f32(exp(score - m_i)) v_s (for
+// head_dim 64 / 128 each of its four waves keeps such a partial over 16
+// positions, and the split's partial merges those four the way the combine
+// merges splits).  The combine forms lse = M + log(sum_i l_i exp(m_i - M))
+// and out = sum_i f32(exp(m_i - lse)) o_i, which equals the reference's
 // sum_s exp(score_s - lse) v_s up to f32 rounding of the factors.
 #include <algorithm>
 #include <cfloat>
+#include <type_traits>
 
 #include "srq_internal.h"
 
@@ -28,8 +31,8 @@ constexpr int kSplit = 64;     // positions per split (two pages)
 constexpr int kMaxGroup = 8;   // query heads per KV head handled together
 constexpr int kMaxHd = 256;
 // Batches up to this many rows use the fused split+merge kernel; larger
-// ones (prefill) the split and combine kernels, whose many workgroups would
-// otherwise each pay the merge's cache write-back and invalidation.
+// ones the split and combine kernels (the same partials and merge order, so
+// the same bits: steps of 1..4 and 5..8 rows agree).
 constexpr int kFusedRows = 4;
 constexpr int kFusedSplits = 16;  // splits of 64 positions: context <= 1024
 static_assert(kFusedSplits <= 64, "the fused kernel's one-wave merge holds one split per lane");
@@ -149,145 +152,296 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const AttnArgs A, float
 }
 
 
-// Fast split kernel for head_dim 64 / 128: every K and V element of the
-// split is loaded by exactly one thread with independent float4 loads, so a
-// split costs one round of memory latency per pass.
-//  scores: thread t -> key t/4 of the split, dims [(t%4)*HD/4, +HD/4)
-//  values: thread t -> dims 4*(t%(HD/4)) .. +3, keys t/(HD/4) + KG*i
+// The fused kernel's split partials travel between workgroups that may sit
+// on different XCDs, each with its own L2.  They are written and read by
+// agent-scope atomic stores and loads (written through to, and read from,
+// the device's coherence point), so publishing them needs no L2 write-back
+// and merging them no L2 invalidation: the writer waits for its stores to
+// complete before it counts its split, and the merger loads only after the
+// count says every split is in.
+template <typename T>
+__device__ __forceinline__ void publish(T *p, T v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <typename T>
+__device__ __forceinline__ T fetch(const T *p) {
+    return __hip_atomic_load(const_cast<T *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// One step of a butterfly over a wave: this lane's value and the value of
+// lane (lane ^ K), by DPP (K = 1, 2, 8), ds_swizzle (K = 4) and the gfx950
+// permlane swaps (K = 16, 32) rather than LDS permutes.  a and b are the two
+// values in some order; op(a, b) equals op(b, a) bit for bit for the sums
+// and maxima below, so every lane holds what a __shfl_xor butterfly gives.
+template <int K>
+__device__ __forceinline__ void xor_pair(int v, int &a, int &b) {
+    if constexpr (K == 1) {
+        a = v, b = __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
+    } else if constexpr (K == 2) {
+        a = v, b = __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, false);  // quad_perm [2,3,0,1]
+    } else if constexpr (K == 4) {
+        a = v, b = __builtin_amdgcn_ds_swizzle(v, 0x101F);  // bit mode, xor mask 4
+    } else if constexpr (K == 8) {
+        a = v, b = __builtin_amdgcn_mov_dpp(v, 0x128, 0xF, 0xF, false);  // row_ror 8
+    } else if constexpr (K == 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+        a = r[0], b = r[1];
+    } else {
+        static_assert(K == 32, "lane distance");
+        const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+        a = r[0], b = r[1];
+    }
+}
+template <int K>
+__device__ __forceinline__ float xor_max(float v) {
+    int a, b;
+    xor_pair<K>(__float_as_int(v), a, b);
+    return fmaxf(__int_as_float(a), __int_as_float(b));
+}
+template <int K>
+__device__ __forceinline__ double xor_add(double v) {
+    const int64_t u = __double_as_longlong(v);
+    int alo, blo, ahi, bhi;
+    xor_pair<K>((int)u, alo, blo);
+    xor_pair<K>((int)(u >> 32), ahi, bhi);
+    const double a = __longlong_as_double((int64_t)(uint32_t)alo | ((int64_t)ahi << 32));
+    const double b = __longlong_as_double((int64_t)(uint32_t)blo | ((int64_t)bhi << 32));
+    return a + b;
+}
+// Maximum and FP64 sum over the 64 lanes, in the order of a __shfl_xor
+// butterfly with distances 32, 16, ..., 1.
+__device__ __forceinline__ float wave_max(float v) {
+    v = xor_max<32>(v), v = xor_max<16>(v), v = xor_max<8>(v);
+    v = xor_max<4>(v), v = xor_max<2>(v), v = xor_max<1>(v);
+    return v;
+}
+__device__ __forceinline__ double wave_sum(double v) {
+    v = xor_add<32>(v), v = xor_add<16>(v), v = xor_add<8>(v);
+    v = xor_add<4>(v), v = xor_add<2>(v), v = xor_add<1>(v);
+    return v;
+}
+
+// LDS of split_partial: the GQA group's queries, each wave's softmax
+// weights and each wave's partial over its 16 keys.
+constexpr int kWaveKeys = kSplit / 4;  // keys per wave
+template <int HD>
+struct SplitStage {
+    alignas(16) float qs[kMaxGroup * HD];
+    alignas(16) float ps[4][kMaxGroup][kWaveKeys];  // [wave][head][key]
+    float wm[4][kMaxGroup];             // wave partials: max,
+    double wl[4][kMaxGroup];            //   FP64 sum,
+    float wo[4][kMaxGroup][HD];         //   weighted V sum
+};
+
+// Partial {m, l, o} of split sp of (row, kv head kh) for every query head of
+// the group, head_dim 64 / 128, 256 threads.  All K and V rows of the split
+// are loaded into registers at once (one round of memory latency).  Wave w
+// takes keys 16w .. 16w+15 of the split for every head of the group:
+//   scores: lane 4k + t holds dims [t*HD/4, +HD/4) of key k; per head a
+//     dot over those dims (FMA in dim order), then the four quarters added
+//     as ((q0 + q1) + (q2 + q3)) by a butterfly, * f32(1/sqrt(hd)); lane
+//     4k + t keeps heads t, t+4
+//   wave softmax per head: m_w = max over its keys, e = exp((double)s - m_w),
+//     l_w = FP64 butterfly sum, p = f32(e)
+//   o_w[j] = sum over its keys of p_k v_k[j], FMA in key order; lane holds
+//     dims HD/64 * lane + ...
+// then wave w merges head w (and w+4) over the four waves, in wave order:
+//   m = max m_w, c_w = exp((double)m_w - m), l = sum l_w c_w (FP64,
+//   butterfly over the four), o[j] = sum f32(c_w) o_w[j] (FMA).
+// Keys past the row's positions weigh nothing.  COHERENT: stored with
+// agent-scope stores (publish) for the fused merge.  Returns false, writing
+// nothing, for a split past the row's positions.
+template <int HD, bool COHERENT>
+__device__ __forceinline__ bool split_partial(const AttnArgs &A, float *part, int nsplit, int row, int kh, int sp,
+                                              SplitStage<HD> &S) {
+    constexpr int QD = HD / 4;    // dims of a key per scoring lane
+    constexpr int DPL = HD / 64;  // V dims per lane
+    typedef typename std::conditional<DPL == 2, float2, float>::type VDims;
+    constexpr int QPT = kMaxGroup * HD / 256;  // query values per thread, at most
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int kvdim = A.kv_heads * HD, G = A.heads / A.kv_heads;
+    // The loads form a chain (row meta -> page table -> K/V): the queries,
+    // which need only the arguments, go first, the row's position and
+    // session together, then both page-table entries of the split together
+    // (the second clamped into the session's row; used only when the split
+    // spans two pages).
+    float qv[QPT];
+#pragma unroll
+    for (int r = 0; r < QPT; ++r) {
+        const int i = tid + 256 * r, g = i / HD, j = i - g * HD;
+        qv[r] = i < G * HD ? A.q[(int64_t)row * A.heads * HD + (int64_t)(kh * G + g) * HD + j] : 0.0f;
+    }
+    const int pos = A.meta.pos[row], sess = A.meta.sess[row];
+    const int s0 = sp * kSplit, pi = s0 / kPageTokens;
+    const int32_t *ptrow = A.meta.pages + (int64_t)sess * A.meta.pt_stride;
+    const int pg0 = ptrow[min(pi, A.meta.pt_stride - 1)], pg1 = ptrow[min(pi + 1, A.meta.pt_stride - 1)];
+    asm volatile("" ::"s"(pos), "s"(pg0), "s"(pg1));  // issue all of them before the exit test
+    const int len = pos + 1, ns = min(len, s0 + kSplit) - s0;
+    if (ns <= 0) return false;
+
+    // Page bases of the split's two pages, then every K and V load at once.
+    const int64_t lay = (int64_t)A.meta.layer * 2 * kPageTokens * kvdim + (int64_t)kh * HD;
+    const float *pb0 = A.meta.kv_pool + (int64_t)pg0 * A.meta.page_elems + lay;
+    const float *pb1 = A.meta.kv_pool + (int64_t)pg1 * A.meta.page_elems + lay;
+    auto key_row = [&](int s, int which) {  // keys past ns read key 0 (finite, weight 0)
+        s = s < ns ? s : 0;
+        const float *pb = s < kPageTokens ? pb0 : pb1;
+        return pb + (int64_t)which * kPageTokens * kvdim + (int64_t)(s & (kPageTokens - 1)) * kvdim;
+    };
+    const int kq = lane >> 2, qt = lane & 3;  // scoring: key kq of the wave, quarter qt
+    const int key0 = kWaveKeys * wave;
+    float4 kr[QD / 4];
+    {
+        const float4 *k = (const float4 *)(key_row(key0 + kq, 0) + qt * QD);
+#pragma unroll
+        for (int u = 0; u < QD / 4; ++u) kr[u] = k[u];
+    }
+    VDims vr[kWaveKeys];
+#pragma unroll
+    for (int k = 0; k < kWaveKeys; ++k) vr[k] = ((const VDims *)key_row(key0 + k, 1))[lane];
+#pragma unroll
+    for (int r = 0; r < QPT; ++r)
+        if (tid + 256 * r < G * HD) S.qs[tid + 256 * r] = qv[r];
+    __syncthreads();
+
+    const float scale = (float)(1.0 / sqrt((double)HD));
+    const bool kvalid = key0 + kq < ns;
+    for (int h0 = 0; h0 < G; h0 += 4) {
+        const int nh = min(4, G - h0);
+        // scores of this lane's key quarter for heads h0 .. h0+3 (slots past
+        // the group repeat its last head, unused)
+        int hs[4];
+#pragma unroll
+        for (int g = 0; g < 4; ++g) hs[g] = min(h0 + g, G - 1);
+        float d[4];
+#pragma unroll
+        for (int g = 0; g < 4; ++g) d[g] = 0.0f;
+#pragma unroll
+        for (int u = 0; u < QD / 4; ++u) {
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const float4 q = ((const float4 *)(S.qs + hs[g] * HD + qt * QD))[u];
+                d[g] = __builtin_fmaf(q.x, kr[u].x, d[g]);
+                d[g] = __builtin_fmaf(q.y, kr[u].y, d[g]);
+                d[g] = __builtin_fmaf(q.z, kr[u].z, d[g]);
+                d[g] = __builtin_fmaf(q.w, kr[u].w, d[g]);
+            }
+        }
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            int a, b;
+            xor_pair<1>(__float_as_int(d[g]), a, b);
+            d[g] = __int_as_float(a) + __int_as_float(b);
+            xor_pair<2>(__float_as_int(d[g]), a, b);
+            d[g] = __int_as_float(a) + __int_as_float(b);
+        }
+        // lane 4k + p: head h0 + p
+        const float sc = (qt == 0 ? d[0] : qt == 1 ? d[1] : qt == 2 ? d[2] : d[3]) * scale;
+        const bool valid = kvalid && qt < nh;
+        float m = valid ? sc : -FLT_MAX;
+        m = xor_max<4>(m), m = xor_max<8>(m), m = xor_max<16>(m), m = xor_max<32>(m);
+        double e = valid ? exp((double)sc - (double)m) : 0.0;
+        double l = e;
+        l = xor_add<4>(l), l = xor_add<8>(l), l = xor_add<16>(l), l = xor_add<32>(l);
+        if (qt < nh) {
+            S.ps[wave][h0 + qt][kq] = (float)e;
+            if (kq == 0) {
+                S.wm[wave][h0 + qt] = m;
+                S.wl[wave][h0 + qt] = l;
+            }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        // o_w of heads h0 .. h0+3 over the wave's keys (slots past the group
+        // repeat its last head and are not stored)
+        float o[4][DPL];
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+#pragma unroll
+            for (int t = 0; t < DPL; ++t) o[g][t] = 0.0f;
+#pragma unroll
+        for (int k4 = 0; k4 < kWaveKeys / 4; ++k4) {
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const float4 pw = ((const float4 *)S.ps[wave][hs[g]])[k4];
+                const float pk[4] = {pw.x, pw.y, pw.z, pw.w};
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    if constexpr (DPL == 2) {
+                        o[g][0] = __builtin_fmaf(pk[r], vr[4 * k4 + r].x, o[g][0]);
+                        o[g][1] = __builtin_fmaf(pk[r], vr[4 * k4 + r].y, o[g][1]);
+                    } else {
+                        o[g][0] = __builtin_fmaf(pk[r], vr[4 * k4 + r], o[g][0]);
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+            if (g < nh)
+#pragma unroll
+                for (int t = 0; t < DPL; ++t) S.wo[wave][h0 + g][DPL * lane + t] = o[g][t];
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+    __syncthreads();
+
+    // wave w merges head w (and w + 4) over the four waves
+    for (int h = wave; h < G; h += 4) {
+        const int src = lane & 3;
+        const float mw = S.wm[src][h];
+        const double lw = S.wl[src][h];
+        const float M = xor_max<2>(xor_max<1>(mw));
+        const double c = exp((double)mw - (double)M);
+        const double l = xor_add<2>(xor_add<1>(lw * c));
+        const float cf = (float)c;
+        float o[DPL];
+#pragma unroll
+        for (int t = 0; t < DPL; ++t) o[t] = 0.0f;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            const float cw = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(cf), w));
+#pragma unroll
+            for (int t = 0; t < DPL; ++t) o[t] = __builtin_fmaf(cw, S.wo[w][h][DPL * lane + t], o[t]);
+        }
+        float *p = partial(part, row, kh * G + h, sp, A.heads, nsplit, HD);
+        if constexpr (COHERENT) {
+            if (lane == 0) {
+                publish(p, M);
+                publish((double *)(p + 2), l);
+            }
+            if constexpr (DPL == 2)
+                publish((uint64_t *)(p + 4) + lane,
+                        (uint64_t)__float_as_uint(o[0]) | ((uint64_t)__float_as_uint(o[1]) << 32));
+            else
+                publish(p + 4 + lane, o[0]);
+        } else {
+            if (lane == 0) {
+                p[0] = M;
+                *(double *)(p + 2) = l;
+            }
+#pragma unroll
+            for (int t = 0; t < DPL; ++t) p[4 + DPL * lane + t] = o[t];
+        }
+    }
+    return true;
+}
+
+// Split kernel for head_dim 64 / 128 (split_partial); the combine kernel
+// merges.  Splits past a row's positions write the empty partial.
 template <int HD>
 __global__ __launch_bounds__(256) void attn_split_fast_kernel(const AttnArgs A, float *__restrict__ part,
                                                               int nsplit) {
-    constexpr int QD = HD / 4;           // dims per scoring thread
-    constexpr int DG = HD / 4;           // float4 dim groups in the value pass
-    constexpr int KG = 256 / DG;         // key groups in the value pass
-    constexpr int KPG = kSplit / KG;     // keys per value thread
-    __shared__ float qs[kMaxGroup * HD];
-    __shared__ float sc[kMaxGroup][kSplit];
-    __shared__ float4 red[KG][kMaxGroup][DG];
-
+    __shared__ SplitStage<HD> S;
     const int row = blockIdx.x, kh = blockIdx.y, sp = blockIdx.z;
-    const int tid = threadIdx.x, lane = tid & 63;
-    const int kvdim = A.kv_heads * HD, G = A.heads / A.kv_heads;
-    const int pos = A.meta.pos[row], sess = A.meta.sess[row];
-    const int len = pos + 1, s0 = sp * kSplit, s1 = min(len, s0 + kSplit), ns = s1 - s0;
-    if (ns <= 0) {
-        for (int i = tid; i < G * (HD + 4); i += 256) {
-            const int g = i / (HD + 4), k = i - g * (HD + 4);
-            float *p = partial(part, row, kh * G + g, sp, A.heads, nsplit, HD);
-            p[k] = k == 0 ? -FLT_MAX : 0.0f;
-        }
-        return;
-    }
-    // Every K and V load of the split at once (one round of memory latency).
-    const int part4 = tid & 3;
-    float4 kr[QD / 4];
-    {
-        const int s = tid >> 2, sk = s < ns ? s : 0;  // clamp: load a valid row, drop below
-        const float *k = kv_row(A.meta, sess, s0 + sk, kvdim, 0) + (int64_t)kh * HD + part4 * QD;
-#pragma unroll
-        for (int u = 0; u < QD / 4; ++u) kr[u] = ((const float4 *)k)[u];
-    }
-    const int dg = tid % DG, kg = tid / DG;
-    float4 vr[KPG];
-#pragma unroll
-    for (int i = 0; i < KPG; ++i) {
-        const int s = kg + KG * i;
-        const int sk = s < ns ? s : 0;
-        vr[i] = ((const float4 *)(kv_row(A.meta, sess, s0 + sk, kvdim, 1) + (int64_t)kh * HD))[dg];
-    }
-    for (int i = tid; i < G * HD; i += 256) {
-        const int g = i / HD, j = i - g * HD;
-        qs[i] = A.q[(int64_t)row * A.heads * HD + (int64_t)(kh * G + g) * HD + j];
-    }
-    // Keep the V loads ahead of the barrier (the compiler would sink them).
-#pragma unroll
-    for (int i = 0; i < KPG; ++i) asm volatile("" ::"v"(vr[i].x), "v"(vr[i].y), "v"(vr[i].z), "v"(vr[i].w));
-    __syncthreads();
-    const float scale = (float)(1.0 / sqrt((double)HD));
-
-    // ---- scores -------------------------------------------------------------
-    {
-        const int s = tid >> 2;
-#pragma unroll
-        for (int g = 0; g < kMaxGroup; ++g) {
-            if (g >= G) break;
-            const float *q = qs + g * HD + part4 * QD;
-            float d = 0.0f;
-#pragma unroll
-            for (int u = 0; u < QD / 4; ++u) {
-                d = __builtin_fmaf(q[4 * u + 0], kr[u].x, d);
-                d = __builtin_fmaf(q[4 * u + 1], kr[u].y, d);
-                d = __builtin_fmaf(q[4 * u + 2], kr[u].z, d);
-                d = __builtin_fmaf(q[4 * u + 3], kr[u].w, d);
-            }
-            d += __shfl_xor(d, 1, 64);
-            d += __shfl_xor(d, 2, 64);
-            if (part4 == 0 && s < ns) sc[g][s] = d * scale;
-        }
-    }
-    __syncthreads();
-
-    // ---- per-head split max and FP64 sum (one wave per head) ----------------
-    const int wave = tid >> 6;
-    for (int g = wave; g < G; g += 4) {
-        float m = -FLT_MAX;
-        if (lane < ns) m = sc[g][lane];
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
-        double e = 0.0;
-        if (lane < ns) {
-            e = exp((double)sc[g][lane] - (double)m);
-            sc[g][lane] = (float)e;
-        }
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) e += __shfl_xor(e, o, 64);
-        if (lane == 0) {
-            float *p = partial(part, row, kh * G + g, sp, A.heads, nsplit, HD);
-            p[0] = m;
-            *(double *)(p + 2) = e;
-        }
-    }
-    __syncthreads();
-
-    // ---- values: every head of the group at once, one tree ------------------
-    {
-        float4 acc[kMaxGroup];
-#pragma unroll
-        for (int g = 0; g < kMaxGroup; ++g) acc[g] = make_float4(0.f, 0.f, 0.f, 0.f);
-        // Per head: its KPG weights are read from LDS together, then the
-        // FMAs (keys in order, as the reduction below expects).
-#pragma unroll
-        for (int g = 0; g < kMaxGroup; ++g) {
-            if (g < G) {
-                float w[KPG];
-#pragma unroll
-                for (int i = 0; i < KPG; ++i) {
-                    const int s = kg + KG * i;
-                    w[i] = s < ns ? sc[g][s] : 0.0f;
-                }
-#pragma unroll
-                for (int i = 0; i < KPG; ++i) {
-                    acc[g].x = __builtin_fmaf(w[i], vr[i].x, acc[g].x);
-                    acc[g].y = __builtin_fmaf(w[i], vr[i].y, acc[g].y);
-                    acc[g].z = __builtin_fmaf(w[i], vr[i].z, acc[g].z);
-                    acc[g].w = __builtin_fmaf(w[i], vr[i].w, acc[g].w);
-                }
-            }
-        }
-#pragma unroll
-        for (int g = 0; g < kMaxGroup; ++g)
-            if (g < G) red[kg][g][dg] = acc[g];
-    }
-    __syncthreads();
-    for (int t = tid; t < G * DG; t += 256) {
-        const int g = t / DG, j = t - g * DG;
-        float4 o = red[0][g][j];
-        for (int k2 = 1; k2 < KG; ++k2) {
-            const float4 u = red[k2][g][j];
-            o.x += u.x, o.y += u.y, o.z += u.z, o.w += u.w;
-        }
+    if (split_partial<HD, false>(A, part, nsplit, row, kh, sp, S)) return;
+    const int G = A.heads / A.kv_heads;
+    for (int i = threadIdx.x; i < G * (HD + 4); i += 256) {
+        const int g = i / (HD + 4), k = i - g * (HD + 4);
         float *p = partial(part, row, kh * G + g, sp, A.heads, nsplit, HD);
-        ((float4 *)(p + 4))[j] = o;
+        p[k] = k == 0 ? -FLT_MAX : 0.0f;
     }
 }
 
@@ -297,61 +451,63 @@ constexpr int kMergeBatch = 16;   // partial loads in flight per (head, dim) pai
 
 // Merge of at most 64 split partials for head h of a row by one wave, with no
 // barrier: the same arithmetic and order as merge_splits below (lane i holds
-// split i's factor; each lane's dims accumulate the splits in order).
-__device__ __forceinline__ void merge_wave(const AttnArgs &A, const float *part, int nsplit, int row, int h, int hd,
+// split i's factor; each dim accumulates the splits in order).  The partials
+// are read with agent-scope loads (publish / fetch); lane holds dims
+// HD/64 * lane + ....
+template <int HD>
+__device__ __forceinline__ void merge_wave(const AttnArgs &A, const float *part, int nsplit, int row, int h,
                                            int used) {
-    // One round of loads: every split's {m, l} (lane = split) and, for
-    // used <= kMergeBatch, the o values of this lane's first two dims.
+    // One round of loads, none of them under a lane condition (that would
+    // make the compiler wait for it before issuing the rest): split
+    // min(lane, used-1)'s {m, l} and, for used <= kMergeBatch, this lane's
+    // dims of every split.
+    constexpr int DL = HD / 64;  // dims per lane
+    typedef typename std::conditional<DL == 2, uint64_t, float>::type Dims;
     const int lane = threadIdx.x & 63;
-    const float *pb = partial((float *)part, row, h, 0, A.heads, nsplit, hd) + 4;
-    float mi = 0.0f;
-    double li = 0.0;
-    if (lane < used) {
-        const float *p = partial((float *)part, row, h, lane, A.heads, nsplit, hd);
-        mi = p[0];
-        li = *(const double *)(p + 2);
-    }
-    float v0[kMergeBatch], v1[kMergeBatch];
+    const float *pb = partial((float *)part, row, h, 0, A.heads, nsplit, HD) + 4 + DL * lane;
+    const float *pl = partial((float *)part, row, h, min(lane, used - 1), A.heads, nsplit, HD);
+    const float mraw = fetch(pl);
+    const double lraw = fetch((const double *)(pl + 2));
+    Dims v[kMergeBatch];
     const bool pre = used <= kMergeBatch;
     if (pre) {
-        const int j0 = min(lane, hd - 1), j1 = min(lane + 64, hd - 1);
 #pragma unroll
-        for (int b = 0; b < kMergeBatch; ++b) {
-            const int64_t off = (int64_t)min(b, used - 1) * (hd + 4);
-            v0[b] = pb[off + j0];
-            v1[b] = pb[off + j1];
-        }
+        for (int b = 0; b < kMergeBatch; ++b)
+            if (b < used) v[b] = fetch((const Dims *)(pb + (int64_t)b * (HD + 4)));
     }
-    float M = lane < used ? mi : -FLT_MAX;
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
-    double l = lane < used ? li * exp((double)mi - (double)M) : 0.0;
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) l += __shfl_xor(l, o, 64);
+    const float M = wave_max(lane < used ? mraw : -FLT_MAX);
+    const double l = wave_sum(lane < used ? lraw * exp((double)mraw - (double)M) : 0.0);
     const double lse = (double)M + log(l);
-    const float cf = lane < used ? (float)exp((double)mi - lse) : 0.0f;
-    for (int j = lane; j < hd; j += 64) {
-        float o = 0.0f;
-        if (pre && j < lane + 128) {
-            const float *v = j == lane ? v0 : v1;
+    const float cf = lane < used ? (float)exp((double)mraw - lse) : 0.0f;
+    float o[DL];
+#pragma unroll
+    for (int d = 0; d < DL; ++d) o[d] = 0.0f;
+    auto acc = [&](float c, Dims w) {
+        if constexpr (DL == 2) {
+            o[0] = __builtin_fmaf(c, __uint_as_float((uint32_t)w), o[0]);
+            o[1] = __builtin_fmaf(c, __uint_as_float((uint32_t)(w >> 32)), o[1]);
+        } else {
+            o[0] = __builtin_fmaf(c, w, o[0]);
+        }
+    };
+    if (pre) {
+#pragma unroll
+        for (int b = 0; b < kMergeBatch; ++b)
+            if (b < used) acc(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(cf), b)), v[b]);
+    } else {
+        for (int i0 = 0; i0 < used; i0 += kMergeBatch) {
+            Dims w[kMergeBatch];
 #pragma unroll
             for (int b = 0; b < kMergeBatch; ++b)
-                if (b < used)
-                    o = __builtin_fmaf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(cf), b)), v[b], o);
-        } else {
-            for (int i0 = 0; i0 < used; i0 += kMergeBatch) {
-                float v[kMergeBatch];
+                if (i0 + b < used) w[b] = fetch((const Dims *)(pb + (int64_t)(i0 + b) * (HD + 4)));
 #pragma unroll
-                for (int b = 0; b < kMergeBatch; ++b) v[b] = pb[(int64_t)min(i0 + b, used - 1) * (hd + 4) + j];
-#pragma unroll
-                for (int b = 0; b < kMergeBatch; ++b)
-                    if (i0 + b < used)
-                        o = __builtin_fmaf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(cf), i0 + b)), v[b],
-                                           o);
-            }
+            for (int b = 0; b < kMergeBatch; ++b)
+                if (i0 + b < used) acc(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(cf), i0 + b)), w[b]);
         }
-        A.out[(int64_t)row * A.heads * hd + (int64_t)h * hd + j] = o;
     }
+    float *out = A.out + (int64_t)row * A.heads * HD + (int64_t)h * HD + DL * lane;
+#pragma unroll
+    for (int d = 0; d < DL; ++d) out[d] = o[d];
 }
 
 // Sum over splits i in [b0, b1) of cf[i] * pb[i * (hd + 4)] added to o by
@@ -497,164 +653,32 @@ __device__ __forceinline__ void merge_splits(const AttnArgs &A, const float *par
     }
 }
 
-// Fused split + combine for decode-sized batches, head_dim 64 / 128.
-// Workgroup (row, kv head, split) loads its K and V rows together (one round
-// of memory latency), scores all query heads of the GQA group, writes its
-// partial {m, l, o}, and the last split of a (row, kv head) to finish merges
-// all partials of the group with the combine rule (counter per (row, kv
-// head), reset by the merging workgroup, so the kernel replays without
-// clearing).
-//  scores: thread t -> key t/4 of the split, dims [(t%4)*HD/4, +HD/4)
-//  values: thread t -> dims 4*(t%(HD/4)) .. +3, keys t/(HD/4) + KG*i
+// Fused split + combine for decode-sized batches, head_dim 64 / 128:
+// workgroup (row, kv head, split) writes its split_partial, and the last
+// split of a (row, kv head) to finish merges all partials of the group with
+// the combine rule (counter per (row, kv head), reset by the merging
+// workgroup, so the kernel replays without clearing).
 template <int HD>
 __global__ __launch_bounds__(256) void attn_fused_kernel(const AttnArgs A, float *__restrict__ part, int nsplit,
                                                          int32_t *__restrict__ counters) {
-    constexpr int QD = HD / 4;        // dims per scoring thread
-    constexpr int DG = HD / 4;        // float4 dim groups in the value pass
-    constexpr int KG = 256 / DG;      // key groups in the value pass
-    constexpr int KPG = kSplit / KG;  // keys per value thread
-    __shared__ float qs[kMaxGroup * HD];
-    __shared__ float sc[kMaxGroup][kSplit];
-    __shared__ float4 red[KG][kMaxGroup][DG];
+    __shared__ SplitStage<HD> S;
     __shared__ int last;
-
     const int row = blockIdx.x, kh = blockIdx.y, sp = blockIdx.z;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int kvdim = A.kv_heads * HD, G = A.heads / A.kv_heads;
-    const int pos = A.meta.pos[row], sess = A.meta.sess[row];
-    const int len = pos + 1, s0 = sp * kSplit, s1 = min(len, s0 + kSplit), ns = s1 - s0;
-    if (ns <= 0) return;  // past the row's positions: no partial, no count
-    const int used = (len + kSplit - 1) / kSplit;
-
-    // Page bases of the split's two pages; then every K and V load at once.
-    const int32_t *pt = A.meta.pages + (int64_t)sess * A.meta.pt_stride + s0 / kPageTokens;
-    const float *pb0 = A.meta.kv_pool + (int64_t)pt[0] * A.meta.page_elems +
-                       (int64_t)A.meta.layer * 2 * kPageTokens * kvdim + (int64_t)kh * HD;
-    const float *pb1 = ns > kPageTokens ? A.meta.kv_pool + (int64_t)pt[1] * A.meta.page_elems +
-                                              (int64_t)A.meta.layer * 2 * kPageTokens * kvdim + (int64_t)kh * HD
-                                        : pb0;
-    auto key_row = [&](int s, int which) {  // s < ns
-        const float *pb = s < kPageTokens ? pb0 : pb1;
-        return pb + (int64_t)which * kPageTokens * kvdim + (int64_t)(s & (kPageTokens - 1)) * kvdim;
-    };
-    const int ks = tid >> 2, part4 = tid & 3;
-    float4 kr[QD / 4];
-    {
-        const float *k = key_row(ks < ns ? ks : 0, 0) + part4 * QD;
-#pragma unroll
-        for (int u = 0; u < QD / 4; ++u) kr[u] = ((const float4 *)k)[u];
-    }
-    const int dg = tid % DG, kg = tid / DG;
-    float4 vr[KPG];
-#pragma unroll
-    for (int i = 0; i < KPG; ++i) {
-        const int sv = kg + KG * i;
-        vr[i] = ((const float4 *)key_row(sv < ns ? sv : 0, 1))[dg];
-    }
-    for (int i = tid; i < G * HD; i += 256) {
-        const int g = i / HD, j = i - g * HD;
-        qs[i] = A.q[(int64_t)row * A.heads * HD + (int64_t)(kh * G + g) * HD + j];
-    }
-    // The V rows are consumed only after the softmax; without this the
-    // compiler sinks their loads past the barrier, which then costs a second
-    // round of memory latency instead of overlapping the K loads.
-#pragma unroll
-    for (int i = 0; i < KPG; ++i) asm volatile("" ::"v"(vr[i].x), "v"(vr[i].y), "v"(vr[i].z), "v"(vr[i].w));
-    __syncthreads();
-    const float scale = (float)(1.0 / sqrt((double)HD));
-
-    // ---- scores -------------------------------------------------------------
-#pragma unroll
-    for (int g = 0; g < kMaxGroup; ++g) {
-        if (g >= G) break;
-        const float *q = qs + g * HD + part4 * QD;
-        float d = 0.0f;
-#pragma unroll
-        for (int u = 0; u < QD / 4; ++u) {
-            d = __builtin_fmaf(q[4 * u + 0], kr[u].x, d);
-            d = __builtin_fmaf(q[4 * u + 1], kr[u].y, d);
-            d = __builtin_fmaf(q[4 * u + 2], kr[u].z, d);
-            d = __builtin_fmaf(q[4 * u + 3], kr[u].w, d);
-        }
-        d += __shfl_xor(d, 1, 64);
-        d += __shfl_xor(d, 2, 64);
-        if (part4 == 0 && ks < ns) sc[g][ks] = d * scale;
-    }
-    __syncthreads();
-
-    // ---- per-head split max and FP64 sum (one wave per head) ----------------
-    for (int g = wave; g < G; g += 4) {
-        float m = -FLT_MAX;
-        if (lane < ns) m = sc[g][lane];
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
-        double e = 0.0;
-        if (lane < ns) {
-            e = exp((double)sc[g][lane] - (double)m);
-            sc[g][lane] = (float)e;
-        }
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) e += __shfl_xor(e, o, 64);
-        if (lane == 0) {
-            float *p = partial(part, row, kh * G + g, sp, A.heads, nsplit, HD);
-            p[0] = m;
-            *(double *)(p + 2) = e;
-        }
-    }
-    __syncthreads();
-
-    // ---- values: every head of the group at once, one tree ------------------
-    {
-        float4 acc[kMaxGroup];
-#pragma unroll
-        for (int g = 0; g < kMaxGroup; ++g) acc[g] = make_float4(0.f, 0.f, 0.f, 0.f);
-        // Per head: its KPG weights are read from LDS together, then the
-        // FMAs (keys in order, as the reduction below expects).
-#pragma unroll
-        for (int g = 0; g < kMaxGroup; ++g) {
-            if (g < G) {
-                float w[KPG];
-#pragma unroll
-                for (int i = 0; i < KPG; ++i) {
-                    const int sv = kg + KG * i;
-                    w[i] = sv < ns ? sc[g][sv] : 0.0f;
-                }
-#pragma unroll
-                for (int i = 0; i < KPG; ++i) {
-                    acc[g].x = __builtin_fmaf(w[i], vr[i].x, acc[g].x);
-                    acc[g].y = __builtin_fmaf(w[i], vr[i].y, acc[g].y);
-                    acc[g].z = __builtin_fmaf(w[i], vr[i].z, acc[g].z);
-                    acc[g].w = __builtin_fmaf(w[i], vr[i].w, acc[g].w);
-                }
-            }
-        }
-#pragma unroll
-        for (int g = 0; g < kMaxGroup; ++g)
-            if (g < G) red[kg][g][dg] = acc[g];
-    }
-    __syncthreads();
-    for (int t = tid; t < G * DG; t += 256) {
-        const int g = t / DG, j = t - g * DG;
-        float4 o = red[0][g][j];
-        for (int k2 = 1; k2 < KG; ++k2) {
-            const float4 u = red[k2][g][j];
-            o.x += u.x, o.y += u.y, o.z += u.z, o.w += u.w;
-        }
-        float *p = partial(part, row, kh * G + g, sp, A.heads, nsplit, HD);
-        ((float4 *)(p + 4))[j] = o;
-    }
-
-    // ---- the last split of (row, kv head) merges ------------------------------
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");  // publish this split's partials
+    const int tid = threadIdx.x, wave = tid >> 6;
+    if (!split_partial<HD, true>(A, part, nsplit, row, kh, sp, S)) return;  // no partial, no count
+    const int G = A.heads / A.kv_heads, used = (A.meta.pos[row] + kSplit) / kSplit;
+    // Each wave's partial stores complete before the barrier, so the split
+    // is counted only once all of them are visible device-wide.
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     int32_t *cnt = counters + (int64_t)row * A.kv_heads + kh;
     if (tid == 0) last = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == used - 1;
     __syncthreads();
     if (!last) return;
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     if (tid == 0) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     // used <= kFusedSplits <= 64: one wave per head merges on its own.
-    for (int g = wave; g < G; g += 4) merge_wave(A, part, nsplit, row, kh * G + g, HD, used);
+    for (int g = wave; g < G; g += 4) merge_wave<HD>(A, part, nsplit, row, kh * G + g, used);
 }
 
 // lse and the weighted sum of split partials for one (row, head); split i
@@ -907,10 +931,8 @@ int launch_attention(hipStream_t s, const AttnArgs &a, float *scratch, int32_t *
         return SRQ_OK;
     }
     if (fast && a.n <= kFusedRows && nsplit <= kFusedSplits) {
-        // Decode-sized batches at short context: one launch, the last split
-        // merges.  Each split then publishes its partials with an agent-scope
-        // release (an L2 writeback on its XCD); past kFusedSplits splits those
-        // cost more than the second launch of split + combine.
+        // Decode-sized batches up to kFusedSplits splits: one launch, the
+        // last split of each (row, kv head) merges.
         if (a.head_dim == 128)
             attn_fused_kernel<128><<<grid, 256, 0, s>>>(a, scratch, nsplit, counters);
         else
