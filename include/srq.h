@@ -88,6 +88,13 @@ int srq_packed_bytes(srq_format fmt, int64_t rows, int64_t cols, int64_t *values
  * ("non-finite HF weight", M:910-912). */
 int srq_pack(srq_exec *e, srq_format fmt, int64_t rows, int64_t cols, const void *src, srq_src_dtype dtype,
              void *values, float *scales);
+/* srq_pack from a host source, as readParam streams host values
+ * (M:857-880): the bytes pass through pinned 16 MiB chunks into device
+ * staging, then pack on the device with identical results.  cancel (host,
+ * nullable) is polled between chunks (the reference's per-chunk context
+ * check, M:894): SRQ_ECANCELED, nothing written. */
+int srq_pack_host(srq_exec *e, srq_format fmt, int64_t rows, int64_t cols, const void *src_host,
+                  srq_src_dtype dtype, void *values, float *scales, const volatile int32_t *cancel);
 
 /* Synthetic initialisation: dst[i] = f32(Normal()*scale) of the reference's
  * RNG seeded with `seed` (RNG{seed}.Normal, M:1411-1439, as NewModel draws
@@ -101,6 +108,9 @@ int srq_fill_normal(srq_exec *e, float *dst, int64_t count, uint64_t seed, doubl
 /* Allocate device storage and pack (Q8/Q4) or convert (F32) from src. */
 int srq_weight_create(srq_exec *e, srq_format fmt, int64_t rows, int64_t cols, const void *src,
                       srq_src_dtype dtype, srq_weight **out);
+/* srq_weight_create from a host source (staged as srq_pack_host). */
+int srq_weight_create_host(srq_exec *e, srq_format fmt, int64_t rows, int64_t cols, const void *src_host,
+                           srq_src_dtype dtype, const volatile int32_t *cancel, srq_weight **out);
 /* Wrap caller-owned packed device storage (not freed by destroy). */
 int srq_weight_wrap(srq_format fmt, int64_t rows, int64_t cols, void *values, float *scales, srq_weight **out);
 int srq_weight_destroy(srq_weight *w);
@@ -179,6 +189,11 @@ enum {
 int srq_model_create(srq_exec *e, const srq_model_config *c, const char *weight_format, srq_model **out);
 /* Load one tensor from device memory (f32/bf16/f16), packing on device. */
 int srq_model_load(srq_model *m, int kind, int layer, const void *src, srq_src_dtype dtype);
+/* readParam (M:857-880): load one tensor from host memory (staged as
+ * srq_pack_host; cancel polled between 16 MiB chunks, SRQ_ECANCELED leaves
+ * the tensor unwritten). */
+int srq_model_load_host(srq_model *m, int kind, int layer, const void *src_host, srq_src_dtype dtype,
+                        const volatile int32_t *cancel);
 int srq_model_destroy(srq_model *m);
 /* hfWeightLayoutFor byte accounting (M:591-619) of the resident weights. */
 int srq_model_resident_bytes(const srq_model *m, int64_t *bytes);
@@ -232,8 +247,11 @@ int srq_cache_read(srq_exec *e, const srq_cache *c, int32_t layer, int32_t pos0,
  * rejected (SRQ_EINVAL).  want (host, nullable) selects sessions whose
  * logits are computed; unselected rows are zeroed (M:6438-6448).  Every
  * argument is validated before anything is mutated; positions are committed
- * only on success.  cancel (host, nullable) is polled between layers:
- * nonzero => SRQ_ECANCELED, no positions committed (M:6213, M:6377).
+ * only on success.  cancel (host, nullable) is polled as layers complete
+ * (M:6213, M:6377): the host then stays at most two layers ahead of the
+ * device, so a flag raised while the step runs stops it within two layers;
+ * nonzero => SRQ_ECANCELED once the layers already queued have drained, no
+ * positions committed.  Without a flag the step is queued whole.
  * logits_host (nullable) receives a host copy. */
 int srq_step(srq_exec *e, srq_model *m, int32_t sessions, srq_cache *const *caches, const int32_t *chunk_lens,
              const int32_t *tokens, const uint8_t *want, float **logits, float *logits_host,

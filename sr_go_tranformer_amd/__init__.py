@@ -60,10 +60,11 @@ def lib():
 EXPORTS = [
     "srq_abi_version", "srq_last_error", "srq_device_count", "srq_alloc", "srq_free", "srq_copy_h2d",
     "srq_copy_d2h", "srq_copy_d2d", "srq_exec_create", "srq_exec_destroy", "srq_exec_synchronize",
-    "srq_exec_stream", "srq_fill_normal", "srq_packed_bytes", "srq_pack", "srq_weight_create", "srq_weight_wrap",
+    "srq_exec_stream", "srq_fill_normal", "srq_packed_bytes", "srq_pack", "srq_pack_host", "srq_weight_create",
+    "srq_weight_create_host", "srq_weight_wrap",
     "srq_weight_destroy", "srq_weight_info", "srq_dequant_rows", "srq_linear", "srq_linear_enqueue",
     "srq_linear_noalloc", "srq_model_create",
-    "srq_model_load", "srq_model_destroy", "srq_model_resident_bytes", "srq_model_weight",
+    "srq_model_load", "srq_model_load_host", "srq_model_destroy", "srq_model_resident_bytes", "srq_model_weight",
     "srq_model_rope_tables", "srq_model_load_safetensors", "srq_archive_check",
     "srq_pool_create", "srq_pool_destroy", "srq_cache_create", "srq_cache_destroy",
     "srq_cache_pos", "srq_cache_read", "srq_step", "srq_argmax", "srq_sample", "srq_decoder_create", "srq_decoder_run",
@@ -90,7 +91,9 @@ def _declare(L):
         "srq_fill_normal": (C.c_int, [P, P, I64, C.c_uint64, C.c_double]),
         "srq_packed_bytes": (C.c_int, [C.c_int, I64, I64, C.POINTER(I64), C.POINTER(I64)]),
         "srq_pack": (C.c_int, [P, C.c_int, I64, I64, P, C.c_int, P, P]),
+        "srq_pack_host": (C.c_int, [P, C.c_int, I64, I64, P, C.c_int, P, P, P]),
         "srq_weight_create": (C.c_int, [P, C.c_int, I64, I64, P, C.c_int, PP]),
+        "srq_weight_create_host": (C.c_int, [P, C.c_int, I64, I64, P, C.c_int, P, PP]),
         "srq_weight_wrap": (C.c_int, [C.c_int, I64, I64, P, P, PP]),
         "srq_weight_destroy": (C.c_int, [P]),
         "srq_weight_info": (C.c_int, [P, C.POINTER(C.c_int), C.POINTER(I64), C.POINTER(I64), PP, PP]),
@@ -100,6 +103,7 @@ def _declare(L):
         "srq_linear_noalloc": (C.c_int, [P, P, P, P, I32]),
         "srq_model_create": (C.c_int, [P, C.POINTER(ModelConfig), C.c_char_p, PP]),
         "srq_model_load": (C.c_int, [P, C.c_int, C.c_int, P, C.c_int]),
+        "srq_model_load_host": (C.c_int, [P, C.c_int, C.c_int, P, C.c_int, P]),
         "srq_model_destroy": (C.c_int, [P]),
         "srq_model_resident_bytes": (C.c_int, [P, C.POINTER(I64)]),
         "srq_model_weight": (C.c_int, [P, C.c_int, C.c_int, PP]),
@@ -249,6 +253,24 @@ def pack(ex, src, fmt, dtype=SRC_F32, cols=None):
     return values, sc.to_numpy(np.float32, (rows, groups))
 
 
+def pack_host(ex, src, fmt, dtype=SRC_F32, cols=None, cancel=None):
+    """pack() through srq_pack_host: the host source is streamed by the
+    library (pinned chunks), not uploaded first.  cancel: an optional
+    ctypes.c_int32 polled between chunks."""
+    src = np.ascontiguousarray(src)
+    rows, cols = src.shape[0], (cols if cols is not None else src.shape[1])
+    vb, sb = packed_bytes(fmt, rows, cols)
+    v, sc = ex.empty(vb), ex.empty(sb)
+    flag = C.byref(cancel) if cancel is not None else None
+    check(lib().srq_pack_host(ex.h, fmt, rows, cols, _np_ptr(src), dtype, v.ptr, sc.ptr, flag))
+    groups = (cols + 63) // 64
+    if fmt == Q8:
+        values = v.to_numpy(np.int8, (rows, cols))
+    else:
+        values = v.to_numpy(np.uint8, (rows, (cols + 1) // 2))
+    return values, sc.to_numpy(np.float32, (rows, groups))
+
+
 class Weight:
     """Param: a device-resident Q8/Q4/F32 matrix [rows, cols]."""
 
@@ -269,6 +291,17 @@ class Weight:
         s = ex.upload(src)
         h = C.c_void_p()
         check(lib().srq_weight_create(ex.h, fmt, rows, cols, s.ptr, dtype, C.byref(h)))
+        return cls(h)
+
+    @classmethod
+    def create_host(cls, ex, src, fmt, dtype=SRC_F32, cols=None, cancel=None):
+        """create() through srq_weight_create_host (host source streamed by
+        the library)."""
+        src = np.ascontiguousarray(src)
+        rows, cols = src.shape[0], (cols if cols is not None else src.shape[1])
+        h = C.c_void_p()
+        flag = C.byref(cancel) if cancel is not None else None
+        check(lib().srq_weight_create_host(ex.h, fmt, rows, cols, _np_ptr(src), dtype, flag, C.byref(h)))
         return cls(h)
 
     @classmethod
@@ -329,7 +362,16 @@ class Model:
         self.h = h
         self.format = weight_format
 
-    def load(self, kind, layer, array, dtype=SRC_F32):
+    def load(self, kind, layer, array, dtype=SRC_F32, cancel=None):
+        """readParam: one tensor from a host array (f32, or uint16 words for
+        SRC_BF16 / SRC_F16) through srq_model_load_host.  cancel: an
+        optional ctypes.c_int32 polled between 16 MiB chunks."""
+        array = np.ascontiguousarray(array)
+        flag = C.byref(cancel) if cancel is not None else None
+        check(lib().srq_model_load_host(self.h, kind, layer, _np_ptr(array), dtype, flag))
+
+    def load_uploaded(self, kind, layer, array, dtype=SRC_F32):
+        """The same tensor uploaded first, then srq_model_load (device source)."""
         buf = self.ex.upload(np.ascontiguousarray(array))
         check(lib().srq_model_load(self.h, kind, layer, buf.ptr, dtype))
 

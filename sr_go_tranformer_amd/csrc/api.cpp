@@ -8,12 +8,14 @@
 // library; there is no CPU fallback.
 #include <algorithm>
 #include <atomic>
+#include <chrono>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
 #include <mutex>
 #include <string>
+#include <thread>
 #include <vector>
 
 #include "srq_internal.h"
@@ -161,6 +163,7 @@ struct srq_exec {
     Workspace ws;
     int32_t *h_meta = nullptr;  // pinned metadata staging
     size_t h_meta_n = 0;
+    hipEvent_t layer_done[2] = {};  // in-flight cancellation: the last layers enqueued
 };
 
 struct srq_weight {
@@ -436,6 +439,8 @@ static void exec_unref(srq_exec *e) {
     if (e->d_err) (void)hipFree(e->d_err);
     if (e->h_err) (void)hipHostFree(e->h_err);
     if (e->h_meta) (void)hipHostFree(e->h_meta);
+    for (hipEvent_t ev : e->layer_done)
+        if (ev) (void)hipEventDestroy(ev);
     if (e->stream) (void)hipStreamDestroy(e->stream);
     delete e;
 }
@@ -786,6 +791,113 @@ int srq_model_load(srq_model *m, int kind, int layer, const void *src, srq_src_d
     return model_join_nonfinite(m, "non-finite HF weight");
 }
 
+// ---------------------------------------------------------- host sources
+// readParam streams a tensor's values from host memory (M:857-880).  Here
+// the source bytes travel through two pinned 16 MiB chunks into one device
+// staging buffer -- the host copy of a chunk overlaps the transfer of the
+// previous one -- and are then packed or converted on the device exactly
+// as a device source is.  cancel (nullable) is polled between chunks.
+namespace {
+constexpr size_t kHostChunk = 16 << 20;
+
+struct HostStage {
+    hipStream_t stream = nullptr;
+    void *dev = nullptr;
+    void *slot[2] = {};
+    hipEvent_t done[2] = {};
+    ~HostStage() {
+        if (stream) (void)hipStreamSynchronize(stream);
+        if (dev) (void)hipFree(dev);
+        for (int i = 0; i < 2; ++i) {
+            if (slot[i]) (void)hipHostFree(slot[i]);
+            if (done[i]) (void)hipEventDestroy(done[i]);
+        }
+    }
+};
+
+int stage_host(hipStream_t stream, const void *src, size_t bytes, const volatile int32_t *cancel, HostStage &hs) {
+    hs.stream = stream;
+    if (hipMalloc(&hs.dev, std::max<size_t>(bytes, 256)) != hipSuccess)
+        return fail(SRQ_ENOMEM, "device staging of %zu bytes does not fit", bytes);
+    const size_t slot_bytes = std::min(bytes, kHostChunk);
+    for (int i = 0; i < 2 && slot_bytes > 0; ++i) {
+        if (hipHostMalloc(&hs.slot[i], slot_bytes, hipHostMallocDefault) != hipSuccess)
+            return fail(SRQ_ENOMEM, "pinned staging of %zu bytes failed", slot_bytes);
+        SRQ_HIP(hipEventCreateWithFlags(&hs.done[i], hipEventDisableTiming));
+    }
+    bool used[2] = {false, false};
+    int chunk = 0;
+    for (size_t pos = 0; pos < bytes; pos += kHostChunk, ++chunk) {
+        if (cancel && *cancel) return fail(SRQ_ECANCELED, "load canceled");
+        const int k = chunk & 1;
+        if (used[k] && hipEventSynchronize(hs.done[k]) != hipSuccess) return fail(SRQ_EDEVICE, "staging copy failed");
+        const size_t len = std::min(kHostChunk, bytes - pos);
+        memcpy(hs.slot[k], (const char *)src + pos, len);
+        if (hipMemcpyAsync((char *)hs.dev + pos, hs.slot[k], len, hipMemcpyHostToDevice, stream) != hipSuccess ||
+            hipEventRecord(hs.done[k], stream) != hipSuccess)
+            return fail(SRQ_EDEVICE, "staging copy failed");
+        used[k] = true;
+    }
+    return SRQ_OK;
+}
+
+size_t src_elem_bytes(int dtype) { return dtype == SRQ_SRC_F32 ? 4 : 2; }
+
+// Element count of tensor (kind, layer) of m, or -1.
+int64_t model_tensor_elems(srq_model *m, int kind, int layer) {
+    const int64_t d = m->c.dim, kd = m->kvdim;
+    const bool in_layer = layer >= 0 && layer < m->c.layers;
+    switch (kind) {
+        case SRQ_T_FINAL_NORM: return d;
+        case SRQ_T_ATTN_NORM:
+        case SRQ_T_FFN_NORM: return in_layer ? d : -1;
+        case SRQ_T_Q_BIAS: return in_layer && m->c.qkv_bias ? d : -1;
+        case SRQ_T_K_BIAS:
+        case SRQ_T_V_BIAS: return in_layer && m->c.qkv_bias ? kd : -1;
+        default: break;
+    }
+    const srq_weight *w = model_matrix(m, kind, layer);
+    return w ? w->rows * w->cols : -1;
+}
+}  // namespace
+
+int srq_pack_host(srq_exec *e, srq_format fmt, int64_t rows, int64_t cols, const void *src_host,
+                  srq_src_dtype dtype, void *values, float *scales, const volatile int32_t *cancel) {
+    if (!e || !src_host || !values || !scales) return fail(SRQ_EINVAL, "null pointer");
+    if (fmt != SRQ_Q8 && fmt != SRQ_Q4) return fail(SRQ_EINVAL, "pack format must be Q8 or Q4");
+    if (rows < 0 || cols < 0 || dtype < SRQ_SRC_F32 || dtype > SRQ_SRC_F16) return fail(SRQ_EINVAL, "bad shape or dtype");
+    DeviceGuard g(e->device);
+    HostStage hs;
+    SRQ_CHECK(stage_host(e->stream, src_host, (size_t)(rows * cols) * src_elem_bytes(dtype), cancel, hs));
+    SRQ_CHECK(launch_pack(e->stream, fmt, rows, cols, hs.dev, dtype, values, scales, e->d_err));
+    return check_err_flag(e, SRQ_ENONFINITE, "non-finite weight in pack source");
+}
+
+int srq_weight_create_host(srq_exec *e, srq_format fmt, int64_t rows, int64_t cols, const void *src_host,
+                           srq_src_dtype dtype, const volatile int32_t *cancel, srq_weight **out) {
+    if (!e || !out || !src_host) return fail(SRQ_EINVAL, "null pointer");
+    *out = nullptr;
+    if (rows <= 0 || cols <= 0 || fmt < SRQ_F32 || fmt > SRQ_Q4 || dtype < SRQ_SRC_F32 || dtype > SRQ_SRC_F16)
+        return fail(SRQ_EINVAL, "bad weight shape, format or dtype");
+    DeviceGuard g(e->device);
+    HostStage hs;
+    SRQ_CHECK(stage_host(e->stream, src_host, (size_t)(rows * cols) * src_elem_bytes(dtype), cancel, hs));
+    return srq_weight_create(e, fmt, rows, cols, hs.dev, dtype, out);
+}
+
+int srq_model_load_host(srq_model *m, int kind, int layer, const void *src_host, srq_src_dtype dtype,
+                        const volatile int32_t *cancel) {
+    if (!m || !src_host) return fail(SRQ_EINVAL, "null pointer");
+    if (dtype < SRQ_SRC_F32 || dtype > SRQ_SRC_F16) return fail(SRQ_EINVAL, "bad source dtype");
+    const int64_t count = model_tensor_elems(m, kind, layer);
+    if (count < 0) return fail(SRQ_EINVAL, "no tensor of kind %d at layer %d", kind, layer);
+    DeviceGuard g(m->device);
+    HostStage hs;
+    SRQ_CHECK(stage_host(m->e->stream, src_host, (size_t)count * src_elem_bytes(dtype), cancel, hs));
+    SRQ_CHECK(model_load_enqueue(m, kind, layer, hs.dev, dtype));
+    return model_join_nonfinite(m, "non-finite HF weight");
+}
+
 int srq_model_rope_tables(const srq_model *m, float *cos_out, float *sin_out) {
     if (!m || !cos_out || !sin_out) return fail(SRQ_EINVAL, "null pointer");
     memcpy(cos_out, m->h_cos.data(), m->h_cos.size() * 4);
@@ -979,6 +1091,23 @@ int ensure_host_meta(srq_exec *e, size_t words) {
     return SRQ_OK;
 }
 
+// In-flight cancellation (the reference checks its context as each layer
+// starts, M:6376-6378): with a cancel flag the host stays at most
+// kLayerWindow layers ahead of the device, polling the flag while it waits
+// for layer l - kLayerWindow to finish, so a flag raised during a step stops
+// it within that many layers.  Without a flag everything is enqueued at once.
+constexpr int kLayerWindow = 2;
+
+static int wait_layer(hipEvent_t ev, const volatile int32_t *cancel) {
+    for (int spins = 0;; ++spins) {
+        const hipError_t q = hipEventQuery(ev);
+        if (q == hipSuccess) return SRQ_OK;
+        if (q != hipErrorNotReady) return fail(SRQ_EDEVICE, "layer wait failed: %s", hipGetErrorString(q));
+        if (*cancel) return fail(SRQ_ECANCELED, "context canceled");
+        if (spins > 64) std::this_thread::sleep_for(std::chrono::microseconds(20));
+    }
+}
+
 // Enqueue the layers of one step for n rows whose metadata is on device.
 int enqueue_layers(srq_exec *e, Workspace &ws, srq_model *m, srq_pool *pool, int32_t n, int32_t max_len,
                    const StepMeta &dm, const volatile int32_t *cancel) {
@@ -1003,7 +1132,11 @@ int enqueue_layers(srq_exec *e, Workspace &ws, srq_model *m, srq_pool *pool, int
     const int nbq = gemv_max_rows(m->L[0].qkv.fmt, d, true, 8 * (int64_t)m->hd + (m->L[0].bias ? d + 2 * kd : 0));
     const int nbg = gemv_max_rows(m->L[0].gu.fmt, d, true, 0);
     if (nbq < 1 || nbg < 1) return fail(SRQ_EINVAL, "model width %lld exceeds the GEMV staging limit", (long long)d);
+    if (cancel)
+        for (hipEvent_t &ev : e->layer_done)
+            if (!ev) SRQ_HIP(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
     for (int l = 0; l < c.layers; ++l) {
+        if (cancel && l >= kLayerWindow) SRQ_CHECK(wait_layer(e->layer_done[l % kLayerWindow], cancel));
         if (cancel && *cancel) return fail(SRQ_ECANCELED, "context canceled");
         Layer &L = m->L[l];
         RowMeta meta = make_meta(e, m, l, dm.pt_stride, dm.pos, dm.sess, dm.pages, pool);
@@ -1106,6 +1239,7 @@ int enqueue_layers(srq_exec *e, Workspace &ws, srq_model *m, srq_pool *pool, int
             g.norm_out = N;
             SRQ_CHECK(launch_gemm(e->stream, g, ws.flags.p, ws.flags.n));
         }
+        if (cancel) SRQ_HIP(hipEventRecord(e->layer_done[l % kLayerWindow], e->stream));
     }
     return SRQ_OK;
 }
