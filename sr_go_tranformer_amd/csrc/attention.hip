@@ -30,12 +30,9 @@ namespace {
 constexpr int kSplit = 64;     // positions per split (two pages)
 constexpr int kMaxGroup = 8;   // query heads per KV head handled together
 constexpr int kMaxHd = 256;
-// Batches up to this many rows use the fused split+merge kernel; larger
-// ones the split and combine kernels (the same partials and merge order, so
-// the same bits: steps of 1..4 and 5..8 rows agree).
-constexpr int kFusedRows = 4;
-constexpr int kFusedSplits = 16;  // splits of 64 positions: context <= 1024
-static_assert(kFusedSplits <= 64, "the fused kernel's one-wave merge holds one split per lane");
+// Batches up to this many rows (the GEMV steps) use the fused split+merge
+// kernel, at any context; larger ones the split and combine kernels.
+constexpr int kFusedRows = 8;
 
 __device__ __forceinline__ const float *kv_row(const RowMeta &m, int sess, int pos, int kvdim, int which) {
     const int page = m.pages[(int64_t)sess * m.pt_stride + pos / kPageTokens];
@@ -446,14 +443,16 @@ __global__ __launch_bounds__(256) void attn_split_fast_kernel(const AttnArgs A, 
 }
 
 constexpr int kMergeChunk = 256;  // splits per pass of the weight table
+constexpr int kChainSplits = 16;  // merge_splits: one FMA chain up to this many splits
 constexpr int kMergePairs = kMaxGroup * kMaxHd / 256;
 constexpr int kMergeBatch = 16;   // partial loads in flight per (head, dim) pair
 
-// Merge of at most 64 split partials for head h of a row by one wave, with no
-// barrier: the same arithmetic and order as merge_splits below (lane i holds
-// split i's factor; each dim accumulates the splits in order).  The partials
-// are read with agent-scope loads (publish / fetch); lane holds dims
-// HD/64 * lane + ....
+// Merge of the split partials for head h of a row by one wave, with no
+// barrier: the same arithmetic and order as merge_splits below for up to 64
+// splits (lane i holds split i's factor; each dim accumulates the splits in
+// order); past 64 each lane first folds its splits lane, lane+64, ... in
+// order.  The partials are read with agent-scope loads (publish / fetch);
+// lane holds dims HD/64 * lane + ....
 template <int HD>
 __device__ __forceinline__ void merge_wave(const AttnArgs &A, const float *part, int nsplit, int row, int h,
                                            int used) {
@@ -475,10 +474,17 @@ __device__ __forceinline__ void merge_wave(const AttnArgs &A, const float *part,
         for (int b = 0; b < kMergeBatch; ++b)
             if (b < used) v[b] = fetch((const Dims *)(pb + (int64_t)b * (HD + 4)));
     }
-    const float M = wave_max(lane < used ? mraw : -FLT_MAX);
-    const double l = wave_sum(lane < used ? lraw * exp((double)mraw - (double)M) : 0.0);
+    float M = lane < used ? mraw : -FLT_MAX;
+    for (int i = lane + 64; i < used; i += 64)
+        M = fmaxf(M, fetch(partial((float *)part, row, h, i, A.heads, nsplit, HD)));
+    M = wave_max(M);
+    double l = lane < used ? lraw * exp((double)mraw - (double)M) : 0.0;
+    for (int i = lane + 64; i < used; i += 64) {
+        const float *p = partial((float *)part, row, h, i, A.heads, nsplit, HD);
+        l += fetch((const double *)(p + 2)) * exp((double)fetch(p) - (double)M);
+    }
+    l = wave_sum(l);
     const double lse = (double)M + log(l);
-    const float cf = lane < used ? (float)exp((double)mraw - lse) : 0.0f;
     float o[DL];
 #pragma unroll
     for (int d = 0; d < DL; ++d) o[d] = 0.0f;
@@ -491,18 +497,26 @@ __device__ __forceinline__ void merge_wave(const AttnArgs &A, const float *part,
         }
     };
     if (pre) {
+        const float cf = lane < used ? (float)exp((double)mraw - lse) : 0.0f;
 #pragma unroll
         for (int b = 0; b < kMergeBatch; ++b)
             if (b < used) acc(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(cf), b)), v[b]);
     } else {
-        for (int i0 = 0; i0 < used; i0 += kMergeBatch) {
-            Dims w[kMergeBatch];
+        for (int c0 = 0; c0 < used; c0 += 64) {
+            // lane i holds the factor of split c0 + i
+            const int ci = min(c0 + lane, used - 1);
+            const float mi = c0 == 0 ? mraw : fetch(partial((float *)part, row, h, ci, A.heads, nsplit, HD));
+            const float cf = c0 + lane < used ? (float)exp((double)mi - lse) : 0.0f;
+            const int cnt = min(64, used - c0);
+            for (int i0 = 0; i0 < cnt; i0 += kMergeBatch) {
+                Dims w[kMergeBatch];
 #pragma unroll
-            for (int b = 0; b < kMergeBatch; ++b)
-                if (i0 + b < used) w[b] = fetch((const Dims *)(pb + (int64_t)(i0 + b) * (HD + 4)));
+                for (int b = 0; b < kMergeBatch; ++b)
+                    if (i0 + b < cnt) w[b] = fetch((const Dims *)(pb + (int64_t)(c0 + i0 + b) * (HD + 4)));
 #pragma unroll
-            for (int b = 0; b < kMergeBatch; ++b)
-                if (i0 + b < used) acc(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(cf), i0 + b)), w[b]);
+                for (int b = 0; b < kMergeBatch; ++b)
+                    if (i0 + b < cnt) acc(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(cf), i0 + b)), w[b]);
+            }
         }
     }
     float *out = A.out + (int64_t)row * A.heads * HD + (int64_t)h * HD + DL * lane;
@@ -597,15 +611,15 @@ __device__ __forceinline__ void merge_splits(const AttnArgs &A, const float *par
     for (int k = 0; k < kMergePairs; ++k) o[k] = 0.0f;
     // Summation order of a (head, dim) pair, fixed by head_dim and the
     // head's split count alone, so a row's output does not depend on the
-    // other rows of its step: up to kFusedSplits splits (and past
-    // kMergeChunk) one FMA chain over the splits in order, the fused
-    // kernel's order; in between, ng groups of consecutive splits, each
-    // summed from zero, then the group sums added in group order.
+    // other rows of its step: up to kChainSplits splits (and past
+    // kMergeChunk) one FMA chain over the splits in order; in between, ng
+    // groups of consecutive splits, each summed from zero, then the group
+    // sums added in group order.
     // GROUPS (the one-head combine of decode-sized batches): the groups run
     // on separate threads, so none idles; otherwise one thread sums its
     // pair's groups one after another, in the same order.
     __shared__ float gs[GROUPS ? 256 : 1];
-    const int ng = hd <= 128 && 256 % hd == 0 && used > kFusedSplits && used <= kMergeChunk ? 256 / hd : 1;
+    const int ng = hd <= 128 && 256 % hd == 0 && used > kChainSplits && used <= kMergeChunk ? 256 / hd : 1;
     for (int c0 = 0; c0 < used; c0 += kMergeChunk) {
         const int cnt = min(kMergeChunk, used - c0);
         for (int t = tid; t < nh * cnt; t += 256) {
@@ -653,17 +667,18 @@ __device__ __forceinline__ void merge_splits(const AttnArgs &A, const float *par
     }
 }
 
-// Fused split + combine for decode-sized batches, head_dim 64 / 128:
-// workgroup (row, kv head, split) writes its split_partial, and the last
-// split of a (row, kv head) to finish merges all partials of the group with
-// the combine rule (counter per (row, kv head), reset by the merging
-// workgroup, so the kernel replays without clearing).
+// Fused split + combine for decode-sized batches, head_dim 64 / 128: 1-D
+// grid, workgroup (row, kv head, split) with row fastest, then kv head.
+// Each writes its split_partial, and the last split of a (row, kv head) to
+// finish merges all partials of the group with the combine rule (counter
+// per (row, kv head), reset by the merging workgroup, so the kernel replays
+// without clearing).
 template <int HD>
 __global__ __launch_bounds__(256) void attn_fused_kernel(const AttnArgs A, float *__restrict__ part, int nsplit,
                                                          int32_t *__restrict__ counters) {
     __shared__ SplitStage<HD> S;
     __shared__ int last;
-    const int row = blockIdx.x, kh = blockIdx.y, sp = blockIdx.z;
+    const int bid = blockIdx.x, row = bid % A.n, kh = (bid / A.n) % A.kv_heads, sp = bid / (A.n * A.kv_heads);
     const int tid = threadIdx.x, wave = tid >> 6;
     if (!split_partial<HD, true>(A, part, nsplit, row, kh, sp, S)) return;  // no partial, no count
     const int G = A.heads / A.kv_heads, used = (A.meta.pos[row] + kSplit) / kSplit;
@@ -677,7 +692,7 @@ __global__ __launch_bounds__(256) void attn_fused_kernel(const AttnArgs A, float
     __syncthreads();
     if (!last) return;
     if (tid == 0) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    // used <= kFusedSplits <= 64: one wave per head merges on its own.
+    // one wave per head merges on its own
     for (int g = wave; g < G; g += 4) merge_wave<HD>(A, part, nsplit, row, kh * G + g, used);
 }
 
@@ -930,13 +945,14 @@ int launch_attention(hipStream_t s, const AttnArgs &a, float *scratch, int32_t *
         SRQ_HIP(hipGetLastError());
         return SRQ_OK;
     }
-    if (fast && a.n <= kFusedRows && nsplit <= kFusedSplits) {
-        // Decode-sized batches up to kFusedSplits splits: one launch, the
-        // last split of each (row, kv head) merges.
+    if (fast && a.n <= kFusedRows) {
+        // Decode-sized batches: one launch, the last split of each (row, kv
+        // head) merges.
+        const dim3 g1((unsigned)((int64_t)a.n * a.kv_heads * nsplit));
         if (a.head_dim == 128)
-            attn_fused_kernel<128><<<grid, 256, 0, s>>>(a, scratch, nsplit, counters);
+            attn_fused_kernel<128><<<g1, 256, 0, s>>>(a, scratch, nsplit, counters);
         else
-            attn_fused_kernel<64><<<grid, 256, 0, s>>>(a, scratch, nsplit, counters);
+            attn_fused_kernel<64><<<g1, 256, 0, s>>>(a, scratch, nsplit, counters);
         SRQ_HIP(hipGetLastError());
         return SRQ_OK;
     }
