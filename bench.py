@@ -71,11 +71,12 @@ class HipEvents:
 
 
 def gemv_roofline(srq, ex, weights, hip, launches, label):
-    """Time the Q8 GEMV (batch 1) over `weights`: `launches` back-to-back
-    launches cycling over the distinct matrices (together far larger than
-    the 256 MB MALL), one HIP event pair on the launch stream around all of
-    them."""
-    rows, cols = weights[0].rows, weights[0].cols
+    """Time the Q8 / Q4 GEMV (batch 1) over `weights`: `launches`
+    back-to-back launches cycling over the distinct matrices (together far
+    larger than the 256 MB MALL), one HIP event pair on the launch stream
+    around all of them."""
+    rows, cols, fmt = weights[0].rows, weights[0].cols, weights[0].fmt
+    tag = {srq.Q8: "q8", srq.Q4: "q4"}[fmt]
     x = ex.empty(cols * 4)
     srq.fill_normal(ex, x, cols, 7, 1.0)
     y = ex.empty(rows * 4)
@@ -93,40 +94,44 @@ def gemv_roofline(srq, ex, weights, hip, launches, label):
     ex.synchronize()
     hip.destroy(a)
     hip.destroy(b)
-    vb, sb = srq.packed_bytes(srq.Q8, rows, cols)
+    vb, sb = srq.packed_bytes(fmt, rows, cols)
     algo = vb + sb + cols * 4 + rows * 4
     avg_s = ms / 1e3 / launches
     achieved = algo / avg_s / 1e9
-    prof_us = read_profile_avg_us("gemv_q8_%dx%d_kernel_trace.txt" % (rows, cols))
+    name = "gemv_%s_%dx%d" % (tag, rows, cols)
+    prof_us = read_profile_avg_us(name + "_kernel_trace.txt",
+                                  "void gemv_stream_kernel<%d, 1, 0, false, true>" % fmt)
     return {
-        "kernel": "gemv_stream_kernel<Q8, n=1, plain> %dx%d (%s)" % (rows, cols, label),
+        "kernel": "gemv_stream_kernel<%s, n=1, plain> %dx%d (%s)" % (tag.upper(), rows, cols, label),
         "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
         "frac": round(achieved / HBM_PEAK_GBS, 4),
-        "traffic": read_traffic("gemv_q8_%dx%d_pmc.txt" % (rows, cols)),
+        "traffic": read_traffic(name + "_pmc.txt"),
         "algorithmic_bytes_per_launch": algo, "avg_launch_us": round(avg_s * 1e6, 3),
         "launches": launches,
         # the committed rocprofv3 summary of the standalone leg (its tracer
         # adds a little per dispatch): same bytes over its average duration
         "profile": None if prof_us is None else {
-            "file": "profiles/gemv_q8_%dx%d_kernel_trace.txt" % (rows, cols), "avg_kernel_us": prof_us,
+            "file": "profiles/%s_kernel_trace.txt" % name, "avg_kernel_us": prof_us,
             "frac": round(algo / (prof_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)},
     }
 
 
-def gemv_only(srq, launches, seed, rows):
-    """The roofline leg alone, for counter runs: standalone Q8 weights
-    rows x 4096 (about 2 GB of distinct matrices) packed on the device,
-    `launches` GEMV launches, then one 256 MiB device-to-device copy whose
-    known byte count calibrates the FETCH_SIZE / WRITE_SIZE counters."""
+def gemv_only(srq, launches, seed, rows, fmt="q8"):
+    """The roofline leg alone, for counter runs: standalone Q8 / Q4 weights
+    rows x 4096 (about 2 GB of distinct packed matrices) packed on the
+    device, `launches` GEMV launches, then one 256 MiB device-to-device copy
+    whose known byte count calibrates the FETCH_SIZE / WRITE_SIZE counters."""
     ex = srq.Executor(0)
     cols = 4096
-    count = max(2, (2 << 30) // (rows * cols))
+    f = {"q8": srq.Q8, "q4": srq.Q4}[fmt]
+    vb, sb = srq.packed_bytes(f, rows, cols)
+    count = max(2, (2 << 30) // (vb + sb))
     src = ex.empty(rows * cols * 4)
     weights = []
     for i in range(count):
         srq.fill_normal(ex, src, rows * cols, seed * 7919 + i, 0.02)
         h = C.c_void_p()
-        srq.check(srq.lib().srq_weight_create(ex.h, srq.Q8, rows, cols, src.ptr, srq.SRC_F32, C.byref(h)))
+        srq.check(srq.lib().srq_weight_create(ex.h, f, rows, cols, src.ptr, srq.SRC_F32, C.byref(h)))
         weights.append(srq.Weight(h))
     src.close()
     ex.synchronize()
@@ -589,7 +594,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--gemv-launches", type=int, default=320)
     ap.add_argument("--config", default="mistral7b-q8-decode",
-                    choices=["mistral7b-q8-decode", "smollm2-q8-decode", "llama1b-q8-gemv-sweep",
+                    choices=["mistral7b-q8-decode", "mistral7b-q4mixed-decode", "smollm2-q8-decode",
+                             "llama1b-q8-gemv-sweep",
                              "mistral7b-q4mixed-prefill", "llama3b-q8-continuous-batching",
                              "mistral7b-q8-longctx-decode", "mistral7b-bf16-archive-load"],
                     help="workload; the default is the headline Mistral-7B Q8 decode")
@@ -602,6 +608,7 @@ def main():
     ap.add_argument("--gemv-only", action="store_true",
                     help="run only the GEMV roofline leg (standalone weights) and a calibration copy")
     ap.add_argument("--gemv-rows", type=int, default=28672, help="--gemv-only: weight rows (4096 columns)")
+    ap.add_argument("--gemv-fmt", default="q8", choices=["q8", "q4"], help="--gemv-only: weight format")
     ap.add_argument("--archive-dir", default=None,
                     help="mistral7b-bf16-archive-load: where the temporary archive is written (default: TMPDIR)")
     ap.add_argument("--eager", action="store_true",
@@ -620,7 +627,7 @@ def main():
     from sr_go_tranformer_amd import synthetic
 
     if args.gemv_only:
-        return gemv_only(srq, args.gemv_launches, args.seed, args.gemv_rows)
+        return gemv_only(srq, args.gemv_launches, args.seed, args.gemv_rows, args.gemv_fmt)
     if args.config == "smollm2-q8-decode":
         return bench_smollm2(srq, args)
     if args.config == "llama1b-q8-gemv-sweep":
@@ -634,10 +641,11 @@ def main():
     if args.config == "mistral7b-bf16-archive-load":
         return bench_archive_load(srq, args)
 
+    fmt = "q4-mixed" if args.config == "mistral7b-q4mixed-decode" else "q8"
     t_start = time.perf_counter()
     ex = srq.Executor(0)
     cfg = synthetic.shape_config("mistral-7b", PROMPT + TOKENS)
-    model = synthetic.build(ex, cfg, "q8", args.seed)
+    model = synthetic.build(ex, cfg, fmt, args.seed)
     build_s = time.perf_counter() - t_start
     resident = model.resident_bytes()
     print("model built in %.1f s, resident %d bytes" % (build_s, resident), file=sys.stderr, flush=True)
@@ -668,7 +676,7 @@ def main():
 
     ms_per_step = decode_ms / args.steps
     tok_s = 1e3 / ms_per_step
-    wbytes = synthetic.decode_weight_bytes(cfg, "q8")
+    wbytes = synthetic.decode_weight_bytes(cfg, fmt)
     gbs = wbytes * tok_s / 1e9
     kd = cfg.dim // cfg.heads * cfg.kv_heads
     pos_mid = PROMPT + args.warmup + args.steps / 2.0
@@ -686,6 +694,22 @@ def main():
           flush=True)
 
     cpu = None
+    if fmt != "q8":
+        tag = "Q4" if fmt == "q4-mixed" else fmt
+        out = {
+            "metric": "Mistral-7B-shape %s decode tokens/s and weight GB/s, batch 1" % fmt,
+            "value": round(tok_s, 2), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+            "ms_per_step": round(ms_per_step, 4), "higher_is_better": True, "dtype": "f32", "data": "synthetic",
+            "config": {"workload": "Mistral-7B shape, %s (layer matrices %s, embedding and head Q8), 128-token "
+                                   "random prompt, %d greedy tokens (%d untimed, %d timed graph-replayed steps)" %
+                                   (fmt, tag, 1 + args.warmup + args.steps, args.warmup, args.steps),
+                       "seed": args.seed, "decode_launch": "eager" if args.eager else "hip-graph"},
+            "weight_bytes_per_token": wbytes, "weight_gb_per_s": round(gbs, 1),
+            "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4), "resident_weight_bytes": resident,
+            "roofline": roof, "gemv_14336x4096": {k: roof_up[k] for k in ("kernel", "achieved", "frac", "traffic",
+                                                                           "avg_launch_us")}}
+        print(json.dumps(out), flush=True)
+        return 0
     if not args.no_cpu_baseline:
         # the oracle decodes the GPU's own token sequence (first + replays)
         n = max(1, min(args.cpu_tokens, len(tokens)))
