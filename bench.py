@@ -100,7 +100,7 @@ def gemv_roofline(srq, ex, weights, hip, launches, label):
     achieved = algo / avg_s / 1e9
     name = "gemv_%s_%dx%d" % (tag, rows, cols)
     prof_us = read_profile_avg_us(name + "_kernel_trace.txt",
-                                  "void gemv_stream_kernel<%d, 1, 0, false, true>" % fmt)
+                                  "void gemv_stream_kernel<%d, 1, 0, false, true," % fmt)
     return {
         "kernel": "gemv_stream_kernel<%s, n=1, plain> %dx%d (%s)" % (tag.upper(), rows, cols, label),
         "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
@@ -144,7 +144,7 @@ def gemv_only(srq, launches, seed, rows, fmt="q8"):
     return 0
 
 
-def read_profile_avg_us(name, kernel_prefix="void gemv_stream_kernel<1, 1, 0, false, true>"):
+def read_profile_avg_us(name, kernel_prefix):
     """Average duration (us) of the roofline kernel in a committed rocprofv3
     --kernel-trace --stats summary."""
     path = os.path.join(ROOT, "profiles", name)
