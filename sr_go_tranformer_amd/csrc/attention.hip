@@ -30,9 +30,14 @@ namespace {
 constexpr int kSplit = 64;     // positions per split (two pages)
 constexpr int kMaxGroup = 8;   // query heads per KV head handled together
 constexpr int kMaxHd = 256;
-// Batches up to this many rows (the GEMV steps) use the fused split+merge
-// kernel, at any context; larger ones the split and combine kernels.
+// Batches up to this many rows (the GEMV steps), over at most kFusedSplits
+// splits, use the fused split+merge kernel; the others the split and
+// combine kernels.  Both merge in the same order (merge_wave follows
+// merge_splits), so which one a step takes does not change its bits.  Past
+// kFusedSplits the fused kernel's one-wave merge of a head is the slower
+// (8k-context decode: 333 against 349 tokens/s).
 constexpr int kFusedRows = 8;
+constexpr int kFusedSplits = 16;
 
 __device__ __forceinline__ const float *kv_row(const RowMeta &m, int sess, int pos, int kvdim, int which) {
     const int page = m.pages[(int64_t)sess * m.pt_stride + pos / kPageTokens];
@@ -448,10 +453,12 @@ constexpr int kMergePairs = kMaxGroup * kMaxHd / 256;
 constexpr int kMergeBatch = 16;   // partial loads in flight per (head, dim) pair
 
 // Merge of the split partials for head h of a row by one wave, with no
-// barrier: the same arithmetic and order as merge_splits below for up to 64
-// splits (lane i holds split i's factor; each dim accumulates the splits in
-// order); past 64 each lane first folds its splits lane, lane+64, ... in
-// order.  The partials are read with agent-scope loads (publish / fetch);
+// barrier.  M, l, the factors and the order of the sums are merge_splits'
+// below, so the fused kernel and the split + combine kernels give the same
+// bits: past 64 splits each lane first folds its splits lane, lane+64, ...
+// in order; each dim accumulates the splits by FMA in split order (lane i
+// holds split i's factor), in the groups merge_splits uses past
+// kChainSplits.  The partials are read with agent-scope loads (publish / fetch);
 // lane holds dims HD/64 * lane + ....
 template <int HD>
 __device__ __forceinline__ void merge_wave(const AttnArgs &A, const float *part, int nsplit, int row, int h,
@@ -502,6 +509,15 @@ __device__ __forceinline__ void merge_wave(const AttnArgs &A, const float *part,
         for (int b = 0; b < kMergeBatch; ++b)
             if (b < used) acc(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(cf), b)), v[b]);
     } else {
+        // merge_splits' order: past kChainSplits (up to kMergeChunk) splits
+        // the dims sum ng groups of `per` consecutive splits, each from
+        // zero, then add the group sums in group order; past kMergeChunk one
+        // chain.  `tot` holds the groups before the current one.
+        static_assert(kMergeBatch == kChainSplits && 256 % HD == 0, "merge_splits' grouping");
+        const int ng = used <= kMergeChunk ? 256 / HD : 1;
+        const int per = (used + ng - 1) / ng;
+        float tot[DL];
+        int next = per, q = 0;
         for (int c0 = 0; c0 < used; c0 += 64) {
             // lane i holds the factor of split c0 + i
             const int ci = min(c0 + lane, used - 1);
@@ -514,10 +530,24 @@ __device__ __forceinline__ void merge_wave(const AttnArgs &A, const float *part,
                 for (int b = 0; b < kMergeBatch; ++b)
                     if (i0 + b < cnt) w[b] = fetch((const Dims *)(pb + (int64_t)(c0 + i0 + b) * (HD + 4)));
 #pragma unroll
-                for (int b = 0; b < kMergeBatch; ++b)
-                    if (i0 + b < cnt) acc(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(cf), i0 + b)), w[b]);
+                for (int b = 0; b < kMergeBatch; ++b) {
+                    if (i0 + b >= cnt) continue;
+                    if (c0 + i0 + b == next) {  // a group ends (wave-uniform)
+#pragma unroll
+                        for (int d = 0; d < DL; ++d) {
+                            tot[d] = q == 0 ? o[d] : tot[d] + o[d];
+                            o[d] = 0.0f;
+                        }
+                        ++q;
+                        next += per;
+                    }
+                    acc(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(cf), i0 + b)), w[b]);
+                }
             }
         }
+        if (q > 0)
+#pragma unroll
+            for (int d = 0; d < DL; ++d) o[d] = tot[d] + o[d];
     }
     float *out = A.out + (int64_t)row * A.heads * HD + (int64_t)h * HD + DL * lane;
 #pragma unroll
@@ -945,7 +975,7 @@ int launch_attention(hipStream_t s, const AttnArgs &a, float *scratch, int32_t *
         SRQ_HIP(hipGetLastError());
         return SRQ_OK;
     }
-    if (fast && a.n <= kFusedRows) {
+    if (fast && a.n <= kFusedRows && nsplit <= kFusedSplits) {
         // Decode-sized batches: one launch, the last split of each (row, kv
         // head) merges.
         const dim3 g1((unsigned)((int64_t)a.n * a.kv_heads * nsplit));

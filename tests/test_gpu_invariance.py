@@ -105,13 +105,13 @@ def _step_alone_and_in_batches(ex, cfg, seed, prompt_n, ns, heads=1, fmt="q8"):
 @pytest.mark.parametrize("prompt_n", [40, 1100])
 def test_step_rows_independent_of_batch(ex, prompt_n):
     """A decode row's logits are bit-identical in steps of 1, 5 and 8 rows
-    (GEMV layers, fused split + merge attention) and in steps of 9, 17, 33,
-    64 and 256 rows (MFMA GEMM layers, split + combine attention), at a
-    short context and past 1024 positions (more than 16 attention splits,
-    where the merge's summation order must not depend on the step's row
-    count).  The head takes the GEMV for up to 16 sessions wanting logits
-    and the GEMM above: within each, the logits do not depend on how many
-    sessions want them."""
+    (GEMV layers) and in steps of 9, 17, 33, 64 and 256 rows (MFMA GEMM
+    layers), at a short context (fused split + merge attention up to 8
+    rows) and past 1024 positions (more than 16 attention splits: split +
+    combine, whose grouped summation order the fused merge shares).  The
+    head takes the GEMV for up to 16 sessions wanting logits and the GEMM
+    above: within each, the logits do not depend on how many sessions want
+    them."""
     print("step invariance", prompt_n, flush=True)
     cfg = srq.make_config(512, 256, 2, 2, 1, 512, 1400, 10000.0, 1e-5, True)
     seed = 5 + prompt_n
@@ -130,8 +130,8 @@ def test_step_rows_independent_of_batch(ex, prompt_n):
 @pytest.mark.parametrize("fmt", ["q8", "q4"])
 def test_step_rows_independent_of_batch_long_context(ex, fmt):
     """Width 1024 (8 heads x 128), Q8 and Q4, at 4200 positions: more than
-    64 attention splits, so the decode merge folds several splits per lane.
-    Steps of 1, 3, 5 and 8 rows give A's row the same bits."""
+    64 attention splits per row.  Steps of 1, 3, 5 and 8 rows give A's row
+    the same bits."""
     print("long-context step invariance", fmt, flush=True)
     cfg = srq.make_config(512, 1024, 2, 8, 2, 1024, 4300, 10000.0, 1e-5, True)
     out = _step_alone_and_in_batches(ex, cfg, 31, 4200, (1, 3, 5, 8), fmt=fmt)
@@ -141,7 +141,7 @@ def test_step_rows_independent_of_batch_long_context(ex, fmt):
 
 def test_multi_session_long_context_steps(ex):
     """Six sessions past 1024 positions decode one token per step together
-    (a 6-row step: fused attention over more than 16 splits); logits
+    (a 6-row step: split + combine attention over more than 16 splits); logits
     against the oracle's step, then greedy continuations identical."""
     cfg = srq.make_config(512, 256, 2, 2, 1, 512, 1400, 10000.0, 1e-5, True)
     m, norms = gpu_models.synthetic(ex, cfg, "q8", 17)
