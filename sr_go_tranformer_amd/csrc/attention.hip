@@ -35,9 +35,10 @@ constexpr int kMaxHd = 256;
 // combine kernels.  Both merge in the same order (merge_wave follows
 // merge_splits), so which one a step takes does not change its bits.  Past
 // kFusedSplits the fused kernel's one-wave merge of a head is the slower
-// (8k-context decode: 333 against 349 tokens/s).
+// (7B decode, fused against split + combine: 425 / 421 tokens/s at 2k
+// context, 376 / 395 at 4k, 325 / 354 at 8k).
 constexpr int kFusedRows = 8;
-constexpr int kFusedSplits = 16;
+constexpr int kFusedSplits = 48;
 
 __device__ __forceinline__ const float *kv_row(const RowMeta &m, int sess, int pos, int kvdim, int which) {
     const int page = m.pages[(int64_t)sess * m.pt_stride + pos / kPageTokens];

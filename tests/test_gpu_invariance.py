@@ -106,9 +106,8 @@ def _step_alone_and_in_batches(ex, cfg, seed, prompt_n, ns, heads=1, fmt="q8"):
 def test_step_rows_independent_of_batch(ex, prompt_n):
     """A decode row's logits are bit-identical in steps of 1, 5 and 8 rows
     (GEMV layers) and in steps of 9, 17, 33, 64 and 256 rows (MFMA GEMM
-    layers), at a short context (fused split + merge attention up to 8
-    rows) and past 1024 positions (more than 16 attention splits: split +
-    combine, whose grouped summation order the fused merge shares).  The
+    layers), at 40 and 1100 positions (attention: fused split + merge up to
+    8 rows, past 16 splits in the combine's grouped summation order).  The
     head takes the GEMV for up to 16 sessions wanting logits and the GEMM
     above: within each, the logits do not depend on how many sessions want
     them."""
@@ -130,8 +129,8 @@ def test_step_rows_independent_of_batch(ex, prompt_n):
 @pytest.mark.parametrize("fmt", ["q8", "q4"])
 def test_step_rows_independent_of_batch_long_context(ex, fmt):
     """Width 1024 (8 heads x 128), Q8 and Q4, at 4200 positions: more than
-    64 attention splits per row.  Steps of 1, 3, 5 and 8 rows give A's row
-    the same bits."""
+    64 attention splits per row (split + combine attention).  Steps of 1,
+    3, 5 and 8 rows give A's row the same bits."""
     print("long-context step invariance", fmt, flush=True)
     cfg = srq.make_config(512, 1024, 2, 8, 2, 1024, 4300, 10000.0, 1e-5, True)
     out = _step_alone_and_in_batches(ex, cfg, 31, 4200, (1, 3, 5, 8), fmt=fmt)
@@ -141,7 +140,7 @@ def test_step_rows_independent_of_batch_long_context(ex, fmt):
 
 def test_multi_session_long_context_steps(ex):
     """Six sessions past 1024 positions decode one token per step together
-    (a 6-row step: split + combine attention over more than 16 splits); logits
+    (a 6-row step: fused attention over more than 16 splits); logits
     against the oracle's step, then greedy continuations identical."""
     cfg = srq.make_config(512, 256, 2, 2, 1, 512, 1400, 10000.0, 1e-5, True)
     m, norms = gpu_models.synthetic(ex, cfg, "q8", 17)
