@@ -355,6 +355,15 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
 constexpr int XLD = 72;
 
+// Workgroup barrier over LDS only.  __syncthreads() also waits for every
+// global load in flight (vmcnt(0)), which in the block loop below would
+// drain the weight and activation loads issued blocks ahead at every block.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 template <int TM>
 struct XTile {
     static constexpr int BM = TM * 16;
@@ -485,9 +494,9 @@ __device__ __forceinline__ float xstore_a(__bf16 *As, int tid, const float4 (&a)
 // Software pipeline, two blocks deep: while the MFMAs of block g run, the
 // wave converts block g+1's codes (loaded two blocks earlier) and splits
 // block g+1's activations into the other LDS stage; blocks g+2 and g+3 are
-// in flight.  Rows past the ends are clamped (weights: scale 0; activations:
-// row n-1, whose outputs are never stored) so the block body has no
-// per-lane branches.
+// in flight.  Rows past the ends are clamped (weights: row rows-1;
+// activations: row n-1) and their outputs are never stored, so the block
+// body has no per-lane branches.
 template <int FMT, int TM, int TN>
 __global__ __launch_bounds__(256, 2) void gemm_x3_kernel(const GemmArgs G, float *__restrict__ partial,
                                                                        int32_t *__restrict__ wflags, const int kper) {
@@ -507,12 +516,10 @@ __global__ __launch_bounds__(256, 2) void gemm_x3_kernel(const GemmArgs G, float
 
     const uint8_t *wp[TN];
     const float *sp[TN];
-    bool wv[TN];
 #pragma unroll
     for (int tn = 0; tn < TN; ++tn) {
         const int64_t row = n0 + tn * 16 + li;
-        wv[tn] = row < G.rows;
-        const int64_t rc = wv[tn] ? row : G.rows - 1;
+        const int64_t rc = row < G.rows ? row : G.rows - 1;
         wp[tn] = (const uint8_t *)G.values + rc * (BB * groups) + (BB / 4) * q;
         sp[tn] = G.scales + rc * groups;
     }
@@ -525,43 +532,67 @@ __global__ __launch_bounds__(256, 2) void gemm_x3_kernel(const GemmArgs G, float
 #pragma unroll
         for (int j = 0; j < TN; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 
+    // JIT (Q8, whose 16-byte code slices leave fewer registers): a block's
+    // codes are converted just before its MFMAs, from weight loads issued
+    // two blocks ahead; otherwise one block ahead, from loads issued three
+    // blocks ahead.
+    constexpr bool JIT = FMT == SRQ_Q8;
+    constexpr int NB = JIT ? 1 : 2;
     R raw[2][TN];
-    float sc[2][TN], s[2][TN];
+    float sc[2][TN], s[NB][TN];
     float4 areg[2][NV];
-    bf16x8 b[2][TN][2];
+    bf16x8 b[NB][TN][2];
+// Loaded values are left untouched until the block is converted: an
+// operation on them here would make the wave wait for the load at once.
+// A clamped (out-of-range) feature row computes on row rows-1's data and is
+// never stored.
 #define SRQ_LOAD_B(g, slot)                                                         \
     _Pragma("unroll") for (int tn = 0; tn < TN; ++tn) {                              \
         raw[slot][tn] = *(const R *)(wp[tn] + (int64_t)(g) * BB);                    \
-        const float sv = sp[tn][(g)];                                                \
-        sc[slot][tn] = wv[tn] ? sv : 0.0f;                                           \
+        sc[slot][tn] = sp[tn][(g)];                                                  \
     }
 #define SRQ_LOAD_A(g, slot) \
     _Pragma("unroll") for (int i = 0; i < NV; ++i) areg[slot][i] = *(const float4 *)(ap + (int64_t)(g) * kBlock + 4 * i);
-#define SRQ_CONVERT(slot)                                                           \
+#define SRQ_CONVERT(slot, dst)                                                      \
     _Pragma("unroll") for (int tn = 0; tn < TN; ++tn) {                              \
-        xcodes<FMT>(raw[slot][tn], b[slot][tn][0], b[slot][tn][1]);                  \
-        s[slot][tn] = sc[slot][tn];                                                  \
+        xcodes<FMT>(raw[slot][tn], b[dst][tn][0], b[dst][tn][1]);                    \
+        s[dst][tn] = sc[slot][tn];                                                   \
     }
 
     SRQ_LOAD_B(gbeg, 0);
     SRQ_LOAD_A(gbeg, 0);
     SRQ_LOAD_B(min(gbeg + 1, glast), 1);
     SRQ_LOAD_A(min(gbeg + 1, glast), 1);
-    SRQ_CONVERT(0);
-    SRQ_LOAD_B(min(gbeg + 2, glast), 0);
+    if constexpr (!JIT) {
+        SRQ_CONVERT(0, 0);
+        SRQ_LOAD_B(min(gbeg + 2, glast), 0);
+    }
     float amax = xstore_a<TM>(As[0], tid, areg[0]);
     SRQ_LOAD_A(min(gbeg + 2, glast), 0);
-    __syncthreads();
+    lds_barrier();
 
+    // Blocks in pairs (the stage index is then a constant).  The second block
+    // of a pair past the slice's end still runs, on the clamped block's data
+    // with a zero scale (adding exactly zero), so that both halves of every
+    // pair wait on the same loads and the loop has no early exit: an exit
+    // after the first half makes the compiler drain every load in flight at
+    // the end of each pair.
     for (int g0 = gbeg; g0 < gend; g0 += 2) {
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
             const int g = g0 + u;
-            if (g >= gend) break;
+            const bool live = g < gend;
             const int v = u ^ 1;
-            // block g+1: codes -> operands, then refill with block g+3
-            SRQ_CONVERT(v);
-            SRQ_LOAD_B(min(g + 3, glast), v);
+            const int bu = JIT ? 0 : u;  // operand slot of block g
+            if constexpr (JIT) {
+                // block g: codes -> operands, then refill with block g+2
+                SRQ_CONVERT(u, 0);
+                SRQ_LOAD_B(min(g + 2, glast), u);
+            } else {
+                // block g+1: codes -> operands, then refill with block g+3
+                SRQ_CONVERT(v, v);
+                SRQ_LOAD_B(min(g + 3, glast), v);
+            }
             const __bf16 *as = As[u];
 #pragma unroll
             for (int tm = 0; tm < TM; ++tm) {
@@ -578,22 +609,23 @@ __global__ __launch_bounds__(256, 2) void gemm_x3_kernel(const GemmArgs G, float
                     for (int t = 2; t >= 0; --t)
 #pragma unroll
                         for (int h = 0; h < 2; ++h)
-                            blk = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[t][h], b[u][tn][h], blk, 0, 0, 0);
+                            blk = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[t][h], b[bu][tn][h], blk, 0, 0, 0);
+                    const float sc_u = live ? s[bu][tn] : 0.0f;
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) acc[tm][tn][r] = __builtin_fmaf(blk[r], s[u][tn], acc[tm][tn][r]);
+                    for (int r = 0; r < 4; ++r) acc[tm][tn][r] = __builtin_fmaf(blk[r], sc_u, acc[tm][tn][r]);
                 }
             }
             // block g+1's activations -> the other stage, then refill with block g+3
             amax = fmaxf(amax, xstore_a<TM>(As[v], tid, areg[v]));
             SRQ_LOAD_A(min(g + 3, glast), v);
-            __syncthreads();
+            lds_barrier();
         }
     }
 #undef SRQ_LOAD_B
 #undef SRQ_LOAD_A
 #undef SRQ_CONVERT
     if (amax > kWideLimit) row_wide[tid / XTile<TM>::TPR] = 1;
-    __syncthreads();
+    lds_barrier();
 
     // D layout of 16x16x32: lane holds rows 4*(lane/16)+r, column lane%16.
     if (partial) {
