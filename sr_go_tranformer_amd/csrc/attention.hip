@@ -30,15 +30,19 @@ namespace {
 constexpr int kSplit = 64;     // positions per split (two pages)
 constexpr int kMaxGroup = 8;   // query heads per KV head handled together
 constexpr int kMaxHd = 256;
-// Batches up to this many rows (the GEMV steps), over at most kFusedSplits
-// splits, use the fused split+merge kernel; the others the split and
-// combine kernels.  Both merge in the same order (merge_wave follows
-// merge_splits), so which one a step takes does not change its bits.  Past
-// kFusedSplits the fused kernel's one-wave merge of a head is the slower
-// (7B decode, fused against split + combine: 425 / 421 tokens/s at 2k
-// context, 376 / 395 at 4k, 325 / 354 at 8k).
-constexpr int kFusedRows = 8;
+// Steps up to this many rows, over at most kFusedSplits splits, use the
+// fused split+merge kernel; the others the split and combine kernels.  Both
+// merge in the same order (merge_wave follows merge_splits), so which one a
+// step takes does not change its bits.  Past kFusedSplits the fused
+// kernel's one-wave merge of a head is the slower (7B decode, fused against
+// split + combine: 425 / 421 tokens/s at 2k context, 376 / 395 at 4k, 325 /
+// 354 at 8k); on 3B continuous-batching steps of up to 64 rows the fused
+// kernel is the faster (1067-1072 against 1060 tokens/s).
+constexpr int kFusedRows = 64;
 constexpr int kFusedSplits = 48;
+// The combine kernel's grouped variant (thread groups sharing a head's
+// split range) serves steps up to this many rows.
+constexpr int kGroupRows = 8;
 
 __device__ __forceinline__ const float *kv_row(const RowMeta &m, int sess, int pos, int kvdim, int which) {
     const int page = m.pages[(int64_t)sess * m.pt_stride + pos / kPageTokens];
@@ -698,7 +702,7 @@ __device__ __forceinline__ void merge_splits(const AttnArgs &A, const float *par
     }
 }
 
-// Fused split + combine for decode-sized batches, head_dim 64 / 128: 1-D
+// Fused split + combine for decode steps, head_dim 64 / 128: 1-D
 // grid, workgroup (row, kv head, split) with row fastest, then kv head.
 // Each writes its split_partial, and the last split of a (row, kv head) to
 // finish merges all partials of the group with the combine rule (counter
@@ -977,8 +981,8 @@ int launch_attention(hipStream_t s, const AttnArgs &a, float *scratch, int32_t *
         return SRQ_OK;
     }
     if (fast && a.n <= kFusedRows && nsplit <= kFusedSplits) {
-        // Decode-sized batches: one launch, the last split of each (row, kv
-        // head) merges.
+        // Decode steps: one launch, the last split of each (row, kv head)
+        // merges.
         const dim3 g1((unsigned)((int64_t)a.n * a.kv_heads * nsplit));
         if (a.head_dim == 128)
             attn_fused_kernel<128><<<g1, 256, 0, s>>>(a, scratch, nsplit, counters);
@@ -994,7 +998,7 @@ int launch_attention(hipStream_t s, const AttnArgs &a, float *scratch, int32_t *
     else
         attn_split_kernel<<<grid, 256, 0, s>>>(a, scratch, nsplit);
     SRQ_HIP(hipGetLastError());
-    if (a.n <= kFusedRows)
+    if (a.n <= kGroupRows)
         attn_combine_kernel<true><<<dim3(a.n, a.heads), 256, 0, s>>>(a, scratch, nsplit, kSplit);
     else
         attn_combine_kernel<false><<<dim3(a.n, a.heads), 256, 0, s>>>(a, scratch, nsplit, kSplit);

@@ -107,7 +107,8 @@ def test_step_rows_independent_of_batch(ex, prompt_n):
     """A decode row's logits are bit-identical in steps of 1, 5 and 8 rows
     (GEMV layers) and in steps of 9, 17, 33, 64 and 256 rows (MFMA GEMM
     layers), at 40 and 1100 positions (attention: fused split + merge up to
-    8 rows, past 16 splits in the combine's grouped summation order).  The
+    64 rows, split + combine for 256, past 16 splits in the combine's
+    grouped summation order).  The
     head takes the GEMV for up to 16 sessions wanting logits and the GEMM
     above: within each, the logits do not depend on how many sessions want
     them."""
