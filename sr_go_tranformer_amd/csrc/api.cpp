@@ -142,9 +142,9 @@ using namespace srq;
 // M:6062-6100).  Captured graphs point into a decoder's own workspace, so a
 // later step that grows the executor's workspace cannot invalidate them.
 struct Workspace {
-    DevBuf X, N, Q, A, T, H, W2, LOG, LOGC, meta, flags, ATT, ATTC, PLAN, SMP;
+    DevBuf X, N, Q, A, T, H, W2, LOG, LOGC, meta, flags, ATT, ATTC, PLAN, SMP, SMPS;
     void release_all() {
-        for (DevBuf *b : {&X, &N, &Q, &A, &T, &H, &W2, &LOG, &LOGC, &meta, &flags, &ATT, &ATTC, &PLAN, &SMP})
+        for (DevBuf *b : {&X, &N, &Q, &A, &T, &H, &W2, &LOG, &LOGC, &meta, &flags, &ATT, &ATTC, &PLAN, &SMP, &SMPS})
             release(*b);
     }
 };
@@ -1393,6 +1393,7 @@ extern "C" int srq_sample(srq_exec *e, const float *logits, int32_t rows, const 
     // [rng: 2*rows][ids: rows][blocked: rows][history_len: rows][row_ids: rows][history]
     const size_t words = (size_t)rows * 6 + hist_words;
     SRQ_CHECK(ensure(ws.SMP, words * 4, e->stream));
+    SRQ_CHECK(ensure(ws.SMPS, sample_scratch_bytes(rows, vocab), e->stream));
     int32_t *d = as<int32_t>(ws.SMP);
     uint64_t *d_rng = (uint64_t *)d;
     int32_t *d_ids = d + 2 * rows, *d_blk = d + 3 * rows, *d_hl = d + 4 * rows, *d_rows = d + 5 * rows;
@@ -1421,7 +1422,7 @@ extern "C" int srq_sample(srq_exec *e, const float *logits, int32_t rows, const 
     a.rng = d_rng;
     a.ids = d_ids;
     a.err = e->d_err;
-    SRQ_CHECK(launch_sample(e->stream, a));
+    SRQ_CHECK(launch_sample(e->stream, a, ws.SMPS.p));
     SRQ_HIP(hipMemcpyAsync(ids, d_ids, (size_t)rows * 4, hipMemcpyDeviceToHost, e->stream));
     SRQ_HIP(hipMemcpyAsync(rng_state, d_rng, (size_t)rows * 8, hipMemcpyDeviceToHost, e->stream));
     SRQ_HIP(hipMemcpyAsync(e->h_err, e->d_err, sizeof(int32_t) * 4, hipMemcpyDeviceToHost, e->stream));

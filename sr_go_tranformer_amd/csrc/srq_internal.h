@@ -198,8 +198,23 @@ struct SampleArgs {
     uint64_t *rng;               // [rows] SplitMix64 states, advanced per draw
     int32_t *ids;                // [rows] out
     int32_t *err;                // |= 1 non-finite logit, 2 no candidate, 4/8 selection limits
+    // Set by launch_sample: rows are cut into `chunks` chunks of chunk_len
+    // ids, each chunk's range and histogram kept in scratch.
+    int32_t chunks, chunk_len;
+    struct SampleRange *range;   // [rows x chunks]
+    unsigned long long *hmass;   // [rows x chunks x 2048]
+    uint32_t *hcount;            // [rows x chunks x 2048]
+    uint32_t *hoff;              // [rows x chunks x 2048] bucket starts in `order`
+    int32_t *order;              // [rows x chunks x chunk_len] a chunk's candidate ids by bucket
 };
-int launch_sample(hipStream_t s, const SampleArgs &a);
+struct SampleRange {  // one chunk of a row
+    double vmax, vmin, best_v;
+    int32_t best_id, cnt, bad, pad;
+    unsigned long long total;  // integer mass (temperature != 0)
+};
+// scratch: sample_scratch_bytes(rows, vocab) bytes, 16-byte aligned.
+int launch_sample(hipStream_t s, const SampleArgs &a, void *scratch);
+size_t sample_scratch_bytes(int32_t rows, int32_t vocab);
 
 // ------------------------------------------------------------- attention
 struct AttnArgs {
