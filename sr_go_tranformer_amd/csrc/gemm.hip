@@ -497,7 +497,7 @@ __device__ __forceinline__ float xstore_a(__bf16 *As, int tid, const float4 (&a)
 // in flight.  Rows past the ends are clamped (weights: row rows-1;
 // activations: row n-1) and their outputs are never stored, so the block
 // body has no per-lane branches.
-template <int FMT, int TM, int TN>
+template <int FMT, int TM, int TN, int KU>
 __global__ __launch_bounds__(256, 2) void gemm_x3_kernel(const GemmArgs G, float *__restrict__ partial,
                                                                        int32_t *__restrict__ wflags, const int kper) {
     constexpr int BM = XTile<TM>::BM, NV = XTile<TM>::NV, PLANE = XTile<TM>::PLANE, XBN = 64 * TN;
@@ -571,26 +571,26 @@ __global__ __launch_bounds__(256, 2) void gemm_x3_kernel(const GemmArgs G, float
     SRQ_LOAD_A(min(gbeg + 2, glast), 0);
     lds_barrier();
 
-    // Blocks in pairs (the stage index is then a constant).  The second block
-    // of a pair past the slice's end still runs, on the clamped block's data
-    // with a zero scale (adding exactly zero), so that both halves of every
-    // pair wait on the same loads and the loop has no early exit: an exit
-    // after the first half makes the compiler drain every load in flight at
-    // the end of each pair.
-    for (int g0 = gbeg; g0 < gend; g0 += 2) {
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-            const int g = g0 + u;
-            const bool live = g < gend;
+    if constexpr (KU > 0) {
+        // One block: its MFMAs on the staged stage u, its codes converted (JIT:
+        // its own; otherwise block g+1's), block g+1's activations split into the
+        // other stage, and the refills of the slots so freed.  Block g runs on
+        // the clamped data of the slice's last block with a zero scale (adding
+        // exactly zero) when `live` is false.  Each slot's refill is kept
+        // after its last use (sched_barrier), so that a refill never overlaps
+        // the value it replaces.
+        auto block = [&](const int g, const int u, const bool live) {
             const int v = u ^ 1;
             const int bu = JIT ? 0 : u;  // operand slot of block g
             if constexpr (JIT) {
                 // block g: codes -> operands, then refill with block g+2
                 SRQ_CONVERT(u, 0);
+                __builtin_amdgcn_sched_barrier(0);
                 SRQ_LOAD_B(min(g + 2, glast), u);
             } else {
                 // block g+1: codes -> operands, then refill with block g+3
                 SRQ_CONVERT(v, v);
+                __builtin_amdgcn_sched_barrier(0);
                 SRQ_LOAD_B(min(g + 3, glast), v);
             }
             const __bf16 *as = As[u];
@@ -617,8 +617,68 @@ __global__ __launch_bounds__(256, 2) void gemm_x3_kernel(const GemmArgs G, float
             }
             // block g+1's activations -> the other stage, then refill with block g+3
             amax = fmaxf(amax, xstore_a<TM>(As[v], tid, areg[v]));
+            __builtin_amdgcn_sched_barrier(0);
             SRQ_LOAD_A(min(g + 3, glast), v);
             lds_barrier();
+        };
+        // Slices of KU blocks (kper == KU), unrolled whole: straight-line
+        // code, so no value is carried around a back edge.  (A loop carries
+        // the ring slots in registers, and the copies the compiler makes of
+        // them at the latch wait for the loads just issued; so does a branch
+        // around a block.)  A shorter last slice runs its missing blocks with
+        // a zero scale.
+#pragma unroll
+        for (int k = 0; k < KU; ++k) block(gbeg + k, k & 1, gbeg + k < gend);
+    } else {
+        // Blocks in pairs (the stage index is then a constant).  The second block
+        // of a pair past the slice's end still runs, on the clamped block's data
+        // with a zero scale (adding exactly zero), so that both halves of every
+        // pair wait on the same loads and the loop has no early exit: an exit
+        // after the first half makes the compiler drain every load in flight at
+        // the end of each pair.
+        for (int g0 = gbeg; g0 < gend; g0 += 2) {
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                const int g = g0 + u;
+                const bool live = g < gend;
+                const int v = u ^ 1;
+                const int bu = JIT ? 0 : u;  // operand slot of block g
+                if constexpr (JIT) {
+                    // block g: codes -> operands, then refill with block g+2
+                    SRQ_CONVERT(u, 0);
+                    SRQ_LOAD_B(min(g + 2, glast), u);
+                } else {
+                    // block g+1: codes -> operands, then refill with block g+3
+                    SRQ_CONVERT(v, v);
+                    SRQ_LOAD_B(min(g + 3, glast), v);
+                }
+                const __bf16 *as = As[u];
+#pragma unroll
+                for (int tm = 0; tm < TM; ++tm) {
+                    bf16x8 a[3][2];
+#pragma unroll
+                    for (int t = 0; t < 3; ++t)
+#pragma unroll
+                        for (int h = 0; h < 2; ++h)
+                            a[t][h] = *(const bf16x8 *)(as + t * PLANE + (tm * 16 + li) * XLD + 16 * q + 8 * h);
+#pragma unroll
+                    for (int tn = 0; tn < TN; ++tn) {
+                        floatx4 blk = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                        for (int t = 2; t >= 0; --t)
+#pragma unroll
+                            for (int h = 0; h < 2; ++h)
+                                blk = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[t][h], b[bu][tn][h], blk, 0, 0, 0);
+                        const float sc_u = live ? s[bu][tn] : 0.0f;
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) acc[tm][tn][r] = __builtin_fmaf(blk[r], sc_u, acc[tm][tn][r]);
+                    }
+                }
+                // block g+1's activations -> the other stage, then refill with block g+3
+                amax = fmaxf(amax, xstore_a<TM>(As[v], tid, areg[v]));
+                SRQ_LOAD_A(min(g + 3, glast), v);
+                lds_barrier();
+            }
         }
     }
 #undef SRQ_LOAD_B
@@ -870,6 +930,16 @@ GemmPlan plan_gemm(int fmt, int32_t n, int64_t rows, int64_t cols) {
     return p;
 }
 
+template <int TN, int KU = 4>
+void launch_unrolled(hipStream_t s, dim3 grid, const GemmArgs &a, float *partial, int32_t *wflags, int kper) {
+    if constexpr (KU <= 12) {
+        if (kper == KU)
+            gemm_x3_kernel<SRQ_Q8, 2, TN, KU><<<grid, 256, 0, s>>>(a, partial, wflags, kper);
+        else
+            launch_unrolled<TN, KU + 1>(s, grid, a, partial, wflags, kper);
+    }
+}
+
 template <int FMT, int BMT>
 void launch_tiles(hipStream_t s, const GemmArgs &a, const GemmPlan &p, float *partial, int32_t *wflags) {
     if constexpr (FMT == SRQ_F32) {
@@ -879,10 +949,17 @@ void launch_tiles(hipStream_t s, const GemmArgs &a, const GemmPlan &p, float *pa
         if (p.x3) {
             const int xbn = 64 * p.tn;
             dim3 grid((unsigned)((a.rows + xbn - 1) / xbn), (unsigned)((a.n + BMT - 1) / BMT), (unsigned)p.slices);
-            if (p.tn == 2)
-                gemm_x3_kernel<FMT, BMT / 16, 2><<<grid, 256, 0, s>>>(a, partial, wflags, p.kper);
-            else
-                gemm_x3_kernel<FMT, BMT / 16, 4><<<grid, 256, 0, s>>>(a, partial, wflags, p.kper);
+            // Q8 slices of 4..12 blocks at 32-row tiles run unrolled
+            if (FMT == SRQ_Q8 && BMT == 32 && p.kper >= 4 && p.kper <= 12) {
+                if (p.tn == 2)
+                    launch_unrolled<2>(s, grid, a, partial, wflags, p.kper);
+                else
+                    launch_unrolled<4>(s, grid, a, partial, wflags, p.kper);
+            } else if (p.tn == 2) {
+                gemm_x3_kernel<FMT, BMT / 16, 2, 0><<<grid, 256, 0, s>>>(a, partial, wflags, p.kper);
+            } else {
+                gemm_x3_kernel<FMT, BMT / 16, 4, 0><<<grid, 256, 0, s>>>(a, partial, wflags, p.kper);
+            }
         } else {
             dim3 grid((unsigned)((a.rows + BN - 1) / BN), (unsigned)((a.n + BMT - 1) / BMT), (unsigned)p.slices);
             gemm_kernel<FMT, BMT><<<grid, 256, 0, s>>>(a, partial, wflags, p.kper);
