@@ -930,13 +930,13 @@ GemmPlan plan_gemm(int fmt, int32_t n, int64_t rows, int64_t cols) {
     return p;
 }
 
-template <int TN, int KU = 4>
+template <int TM, int TN, int KU = 4>
 void launch_unrolled(hipStream_t s, dim3 grid, const GemmArgs &a, float *partial, int32_t *wflags, int kper) {
     if constexpr (KU <= 12) {
         if (kper == KU)
-            gemm_x3_kernel<SRQ_Q8, 2, TN, KU><<<grid, 256, 0, s>>>(a, partial, wflags, kper);
+            gemm_x3_kernel<SRQ_Q8, TM, TN, KU><<<grid, 256, 0, s>>>(a, partial, wflags, kper);
         else
-            launch_unrolled<TN, KU + 1>(s, grid, a, partial, wflags, kper);
+            launch_unrolled<TM, TN, KU + 1>(s, grid, a, partial, wflags, kper);
     }
 }
 
@@ -949,12 +949,12 @@ void launch_tiles(hipStream_t s, const GemmArgs &a, const GemmPlan &p, float *pa
         if (p.x3) {
             const int xbn = 64 * p.tn;
             dim3 grid((unsigned)((a.rows + xbn - 1) / xbn), (unsigned)((a.n + BMT - 1) / BMT), (unsigned)p.slices);
-            // Q8 slices of 4..12 blocks at 32-row tiles run unrolled
-            if (FMT == SRQ_Q8 && BMT == 32 && p.kper >= 4 && p.kper <= 12) {
+            // Q8 slices of 4..12 blocks run unrolled
+            if (FMT == SRQ_Q8 && p.kper >= 4 && p.kper <= 12) {
                 if (p.tn == 2)
-                    launch_unrolled<2>(s, grid, a, partial, wflags, p.kper);
+                    launch_unrolled<BMT / 16, 2>(s, grid, a, partial, wflags, p.kper);
                 else
-                    launch_unrolled<4>(s, grid, a, partial, wflags, p.kper);
+                    launch_unrolled<BMT / 16, 4>(s, grid, a, partial, wflags, p.kper);
             } else if (p.tn == 2) {
                 gemm_x3_kernel<FMT, BMT / 16, 2, 0><<<grid, 256, 0, s>>>(a, partial, wflags, p.kper);
             } else {
