@@ -824,14 +824,21 @@ __device__ __forceinline__ void unit_epilogue(const GemvArgs &A, const Unit &t, 
 // RS (EPI_RESID, at most kResidUnits units per wave): the residual values of
 // the wave's units are loaded once, ahead of the prefetch, and kept in LDS,
 // instead of one residual load per step riding in the weight stream.
-template <int FMT, int NB, int EPI, bool NORM, bool WMAJOR, int G, bool RS>
+//
+// RG: units whose rows a step streams together (their chunks share one read
+// of the activations from LDS: with 4 or 8 batch rows the per-unit LDS reads
+// bound the kernel).  Waves are dealt groups of RG consecutive units; a
+// group past the last unit repeats the last unit's rows and writes nothing.
+// Every row's arithmetic is that of RG = 1.
+template <int FMT, int NB, int EPI, bool NORM, bool WMAJOR, int G, bool RS, int RG = 1>
 __global__ __launch_bounds__(kStreamThreads) void gemv_stream_kernel(const GemvArgs A) {
     using Ly = Lay<FMT, true>;
-    constexpr int E = Ly::E, CW = Ly::CW, R = unit_rows_of<EPI>();
+    constexpr int E = Ly::E, CW = Ly::CW, R1 = unit_rows_of<EPI>(), R = R1 * RG;  // R: rows per step
     // 8 row loads in flight per lane (two waves per SIMD, eight per CU).
     constexpr int P = 8 / R;
     static_assert(P % G == 0 && (G == 1 || (WMAJOR && FMT != SRQ_F32)), "scale groups fill the prefetch ring");
     static_assert(!RS || EPI == EPI_RESID, "staged residuals belong to the residual epilogue");
+    static_assert(!RS || RG == 1, "staged residuals are per unit");
     extern __shared__ __attribute__((aligned(16))) float lds[];  // 16 B: ds_read_b128
     __shared__ StreamSmem sm;
     // The wave index is uniform: make it scalar so the step loop and its
@@ -844,7 +851,8 @@ __global__ __launch_bounds__(kStreamThreads) void gemv_stream_kernel(const GemvA
     float *xs = lds + L.x;
 
     const int64_t rb = row_bytes(FMT, cols), sgroups = groups_of(cols);
-    const int U = unit_count<EPI>(A);
+    const int UU = unit_count<EPI>(A);  // units
+    const int U = RG == 1 ? UU : (UU + RG - 1) / RG;  // the groups dealt to waves
     if (U == 0) return;  // grid-uniform: no rows, nothing to load or write
     // Units are dealt round-robin (u = wid + k*nwaves): at any moment the
     // waves together sweep one contiguous band of rows, which spreads the
@@ -877,21 +885,24 @@ __global__ __launch_bounds__(kStreamThreads) void gemv_stream_kernel(const GemvA
     int lch = 0;
     const uint8_t *lw[R];
     const float *ls[R];
-    const float *lres = nullptr;
+    const float *lres[RG] = {};
     auto set_rows = [&](int u) {
-        const Unit t = unit_rows<EPI>(A, u);
 #pragma unroll
-        for (int i = 0; i < R; ++i) {
-            lw[i] = W + (uint64_t)(uint32_t)t.r[i] * (uint64_t)rb;
-            ls[i] = FMT == SRQ_F32 ? nullptr : A.scales + (uint64_t)(uint32_t)t.r[i] * (uint64_t)sgroups;
+        for (int k = 0; k < RG; ++k) {
+            const Unit t = unit_rows<EPI>(A, RG == 1 ? u : min(u * RG + k, UU - 1));
+#pragma unroll
+            for (int i = 0; i < R1; ++i) {
+                lw[k * R1 + i] = W + (uint64_t)(uint32_t)t.r[i] * (uint64_t)rb;
+                ls[k * R1 + i] = FMT == SRQ_F32 ? nullptr : A.scales + (uint64_t)(uint32_t)t.r[i] * (uint64_t)sgroups;
+            }
+            if constexpr (EPI == EPI_RESID) lres[k] = res_row + t.r[0];
         }
-        if constexpr (EPI == EPI_RESID) lres = res_row + t.r[0];
     };
     uint4 wb[P][R];
     float sb[P][R];
-    float eb[P];  // EPI_RESID: the unit's residual value, carried with each step
+    float eb[P][RG];  // EPI_RESID: the units' residual values, carried with each step
     // group_start: constant once the ring is unrolled (slot % G == 0).
-    auto load_next = [&](uint4(&w)[R], float(&sc)[R], float &e, const bool group_start) {
+    auto load_next = [&](uint4(&w)[R], float(&sc)[R], float(&e)[RG], const bool group_start) {
         const bool ok = (int64_t)lch * CW + (int64_t)lane * E < cols;
         const int boff = ok ? lch * 1024 + lane * 16 : 0;
         // G > 1: lane l loads scale l of the group (l mod G*SPC: Q8 with
@@ -908,7 +919,10 @@ __global__ __launch_bounds__(kStreamThreads) void gemv_stream_kernel(const GemvA
                 sc[i] = 1.0f;
             }
         }
-        if constexpr (EPI == EPI_RESID && !RS) e = *lres;
+        if constexpr (EPI == EPI_RESID && !RS) {
+#pragma unroll
+            for (int k = 0; k < RG; ++k) e[k] = *lres[k];
+        }
         if (lch + 1 < nch) {
             ++lch;
         } else if (lu < ulast) {
@@ -1008,8 +1022,10 @@ __global__ __launch_bounds__(kStreamThreads) void gemv_stream_kernel(const GemvA
                     }
                 }
             }
-            // this step's residual (RS: the unit's staged value), read before the slot is refilled
-            const float resid = RS ? (lane < NB ? rsl[kk * NB + lane] : 0.0f) : eb[k];
+            // this step's residuals (RS: the unit's staged value), read before the slot is refilled
+            float resid[RG];
+#pragma unroll
+            for (int gq = 0; gq < RG; ++gq) resid[gq] = RS ? (lane < NB ? rsl[kk * NB + lane] : 0.0f) : eb[k][gq];
             load_next(wb[k], sb[k], eb[k], k % G == 0);
             if (!live) continue;
             const bool done = ch == nch - 1;
@@ -1023,30 +1039,34 @@ __global__ __launch_bounds__(kStreamThreads) void gemv_stream_kernel(const GemvA
             }
             if (!done) continue;
 
-            // Unit complete: reduce and write.
-            const Unit t = unit_rows<EPI>(A, udone);
-            float v[R][NB];
+            // Units complete: reduce and write.
 #pragma unroll
-            for (int i = 0; i < R; ++i)
+            for (int gq = 0; gq < RG; ++gq) {
+                const int uq = RG == 1 ? udone : udone * RG + gq;
+                const Unit t = unit_rows<EPI>(A, uq);
+                float v[R1][NB];
 #pragma unroll
-                for (int b = 0; b < NB; ++b) {
-                    v[i][b] = dpp_sum(acc[i][b]);
-                    acc[i][b] = 0.0f;
-                }
-            unit_epilogue<EPI, NB, R>(A, t, v, lds, L, sm, resid, lane, fast_row);
+                for (int i = 0; i < R1; ++i)
+#pragma unroll
+                    for (int b = 0; b < NB; ++b) {
+                        v[i][b] = dpp_sum(acc[gq * R1 + i][b]);
+                        acc[gq * R1 + i][b] = 0.0f;
+                    }
+                if (RG == 1 || uq < UU) unit_epilogue<EPI, NB, R1>(A, t, v, lds, L, sm, resid[gq], lane, fast_row);
+            }
         }
     }
 
     // FP64 pass for batch rows holding |x| > kWideLimit (M:4356-4382):
     // Sum_g f64(scale_g) * Sum_j f64(x_j) * f64(w_j), then the epilogue.
     if (!wmask) return;
-    for (int u = wid; u < U; u += nwaves) {
+    for (int u = wid; u < UU; u += nwaves) {
         const Unit t = unit_rows<EPI>(A, u);
-        float v[R][NB] = {};
+        float v[R1][NB] = {};
         for (int b = 0; b < NB; ++b) {
             if (!((wmask >> b) & 1)) continue;
 #pragma unroll
-            for (int i = 0; i < R; ++i) {
+            for (int i = 0; i < R1; ++i) {
                 const uint8_t *wr = W + (int64_t)t.r[i] * rb;
                 double d = 0.0;
                 for (int64_t c = lane * 4; c < cols; c += 256) {
@@ -1062,7 +1082,7 @@ __global__ __launch_bounds__(kStreamThreads) void gemv_stream_kernel(const GemvA
             }
         }
         const float resid = EPI == EPI_RESID && lane < A.n ? A.residual[(int64_t)lane * A.y_stride + t.r[0]] : 0.0f;
-        unit_epilogue<EPI, NB, R>(A, t, v, lds, L, sm, resid, lane, !fast_row);
+        unit_epilogue<EPI, NB, R1>(A, t, v, lds, L, sm, resid, lane, !fast_row);
     }
 }
 
@@ -1095,23 +1115,34 @@ constexpr size_t kMaxLds = 150 * 1024;
 // The streaming kernel variant for a row layout: wave-major dealing for rows
 // of whole 1 KiB chunks, with as many chunks per scale load as divide the row
 // (Q8 4 or 2, Q4 2; a chunk holds 16 or 32 blocks).
-template <int FMT, int NB, int EPI, bool NORM, bool RS>
+template <int FMT, int NB, int EPI, bool NORM, bool RS, int RG = 1>
 int launch_grid(hipStream_t s, const GemvArgs &a, int nch, int64_t blocks) {
     const size_t lds = (size_t)stream_lds<NB, EPI, NORM, RS>(a, nch * Lay<FMT, true>::CW).total * sizeof(float);
     if (lds > kMaxLds)
         return fail(SRQ_EINVAL, "gemv: activation rows do not fit LDS (n=%d cols=%lld)", NB, (long long)a.cols);
     const dim3 grid((unsigned)blocks);
+    // chunks per scale load, at most the prefetch ring's steps
+    constexpr int P = 8 / (unit_rows_of<EPI>() * RG), GQ = FMT == SRQ_Q8 ? 4 : 2;
     if (row_bytes(FMT, a.cols) % 1024 != 0) {
-        gemv_stream_kernel<FMT, NB, EPI, NORM, false, 1, RS><<<grid, kStreamThreads, lds, s>>>(a);
+        gemv_stream_kernel<FMT, NB, EPI, NORM, false, 1, RS, RG><<<grid, kStreamThreads, lds, s>>>(a);
     } else if constexpr (FMT == SRQ_F32) {
-        gemv_stream_kernel<FMT, NB, EPI, NORM, true, 1, RS><<<grid, kStreamThreads, lds, s>>>(a);
+        gemv_stream_kernel<FMT, NB, EPI, NORM, true, 1, RS, RG><<<grid, kStreamThreads, lds, s>>>(a);
     } else {
-        if (FMT == SRQ_Q8 && nch % 4 == 0)
-            gemv_stream_kernel<FMT, NB, EPI, NORM, true, (FMT == SRQ_Q8 ? 4 : 2), RS><<<grid, kStreamThreads, lds, s>>>(a);
-        else if (nch % 2 == 0)
-            gemv_stream_kernel<FMT, NB, EPI, NORM, true, 2, RS><<<grid, kStreamThreads, lds, s>>>(a);
-        else
-            gemv_stream_kernel<FMT, NB, EPI, NORM, true, 1, RS><<<grid, kStreamThreads, lds, s>>>(a);
+        if constexpr (GQ == 4 && P % 4 == 0) {
+            if (nch % 4 == 0) {
+                gemv_stream_kernel<FMT, NB, EPI, NORM, true, 4, RS, RG><<<grid, kStreamThreads, lds, s>>>(a);
+                SRQ_HIP(hipGetLastError());
+                return SRQ_OK;
+            }
+        }
+        if constexpr (P % 2 == 0) {
+            if (nch % 2 == 0) {
+                gemv_stream_kernel<FMT, NB, EPI, NORM, true, 2, RS, RG><<<grid, kStreamThreads, lds, s>>>(a);
+                SRQ_HIP(hipGetLastError());
+                return SRQ_OK;
+            }
+        }
+        gemv_stream_kernel<FMT, NB, EPI, NORM, true, 1, RS, RG><<<grid, kStreamThreads, lds, s>>>(a);
     }
     SRQ_HIP(hipGetLastError());
     return SRQ_OK;
@@ -1141,6 +1172,19 @@ int launch_t(hipStream_t s, const GemvArgs &a) {
             const bool rs = (units + blocks * kStreamWaves - 1) / (blocks * kStreamWaves) <= kResidUnits &&
                             (size_t)stream_lds<NB, EPI, NORM, true>(a, nch * Ly::CW).total * sizeof(float) <= kMaxLds;
             if (rs) return launch_grid<FMT, NB, EPI, NORM, true>(s, a, nch, blocks);
+        }
+        // 4-8 batch rows: row groups when there are groups for every wave, as
+        // large as the registers hold without spilling (4 batch rows: 4
+        // one-row units or 2 pairs; 8 batch rows: 2 one-row units).
+        if constexpr (NB >= 4 && FMT != SRQ_F32) {
+            constexpr int RGM = NB == 4 ? 4 / unit_rows_of<EPI>() : unit_rows_of<EPI>() == 1 ? 2 : 1;
+            const int64_t waves = blocks * kStreamWaves;
+            if constexpr (RGM >= 4) {
+                if (units >= 4 * waves) return launch_grid<FMT, NB, EPI, NORM, false, 4>(s, a, nch, blocks);
+            }
+            if constexpr (RGM >= 2) {
+                if (units >= 2 * waves) return launch_grid<FMT, NB, EPI, NORM, false, 2>(s, a, nch, blocks);
+            }
         }
         return launch_grid<FMT, NB, EPI, NORM, false>(s, a, nch, blocks);
     } else {

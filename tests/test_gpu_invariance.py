@@ -127,6 +127,17 @@ def test_step_rows_independent_of_batch(ex, prompt_n):
     assert same_bits(many[40][64], many[17][64]) and same_bits(many[40][256], many[17][64])
 
 
+def test_step_rows_independent_of_batch_row_groups(ex):
+    """Steps of 5 and 8 rows stream the 4100-unit gate/up GEMV two units
+    per step and the 8200-id head four rows per step (row groups, the last
+    group ragged); a decode row's logits keep the bits of a 1-row step."""
+    print("row-group step invariance", flush=True)
+    cfg = srq.make_config(8200, 256, 1, 2, 1, 4100, 300, 10000.0, 1e-5, True)
+    out = _step_alone_and_in_batches(ex, cfg, 23, 40, (1, 5, 8), heads=6)
+    for n in (5, 8):
+        assert same_bits(out[n], out[1]), n
+
+
 @pytest.mark.parametrize("fmt", ["q8", "q4"])
 def test_step_rows_independent_of_batch_long_context(ex, fmt):
     """Width 1024 (8 heads x 128), Q8 and Q4, at 4200 positions: more than

@@ -192,6 +192,27 @@ def test_linear_gemv_shapes(ex, fmt, shape, n):
     assert np.array_equal(one.view(np.uint32), got[n - 1:n].view(np.uint32))
 
 
+@pytest.mark.parametrize("shape", [(8197, 128), (16390, 1024)])
+@pytest.mark.parametrize("n", [4, 5, 8])
+def test_linear_gemv_row_groups(ex, shape, n):
+    """Q8 GEMV with 4-8 batch rows over 8192+ output rows streams 4 rows
+    per step against one read of the activations (row groups), the last
+    group ragged (rows not a multiple of 4), rows of one chunk and of
+    eight.  Against the oracle, and each batch row's bits equal those of
+    its own 1-row launch (one row per step)."""
+    print("gemv row groups", shape, n, flush=True)
+    rows, cols = shape
+    rng = oracle.RNG(77 + rows + n)
+    dense = rng.fill_normal(rows * cols, 0.02).reshape(rows, cols)
+    x = rng.fill_normal(n * cols, 1.0).reshape(n, cols)
+    w, ow = _weights(ex, dense, srq.Q8)
+    got = srq.linear(ex, w, x)
+    near(got, oracle.linear(ow, x, workers=8))
+    for k in range(n):
+        one = srq.linear(ex, w, x[k:k + 1])
+        assert np.array_equal(one.view(np.uint32), got[k:k + 1].view(np.uint32)), k
+
+
 @pytest.mark.parametrize("fmt", [srq.Q8, srq.Q4, srq.F32])
 @pytest.mark.parametrize("n", [17, 32, 33, 64, 100, 256])
 @pytest.mark.parametrize("shape", [(640, 2048), (1000, 256), (300, 8192), (301, 2048)])
