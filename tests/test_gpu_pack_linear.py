@@ -234,6 +234,30 @@ def test_linear_gemm_mfma(ex, fmt, n, shape):
     assert np.array_equal(got2.view(np.uint32), got[perm].view(np.uint32))
 
 
+# (rows, cols) -> K slices of 5..12 64-input blocks (the Q8 kernel's
+# unrolled instantiations), last slices ragged, 1000 rows a partial tile;
+# 16384 rows take 256-feature tiles.
+UNROLLED_SHAPES = [(3072, 3072), (4096, 3072), (5120, 3072), (4096, 4096), (8192, 2304), (5120, 4096),
+                   (6144, 4096), (3072, 8192), (16384, 3072), (1000, 704)]
+
+
+@pytest.mark.parametrize("shape", UNROLLED_SHAPES)
+def test_linear_gemm_unrolled_slices(ex, shape):
+    """Q8 GEMM whose K slices hold 5..12 blocks, at 20 rows (32-row tiles)
+    and 48 rows (64-row tiles): against the oracle, and the 20 rows keep
+    their bits in the 48-row launch."""
+    print("gemm unrolled", shape, flush=True)
+    rows, cols = shape
+    rng = oracle.RNG(5000 + rows + cols)
+    dense = rng.fill_normal(rows * cols, 0.02).reshape(rows, cols)
+    x = rng.fill_normal(48 * cols, 1.0).reshape(48, cols)
+    w, ow = _weights(ex, dense, srq.Q8)
+    got20 = srq.linear(ex, w, x[:20])
+    near(got20, oracle.linear(ow, x[:20], workers=16))
+    got48 = srq.linear(ex, w, x)
+    assert np.array_equal(got48[:20].view(np.uint32), got20.view(np.uint32))
+
+
 @pytest.mark.parametrize("shape", [(200, 1024, 40), (200, 1024, 20), (1000, 256, 40), (1000, 256, 20)])
 def test_linear_gemm_wide_rows(ex, shape):
     """Wide rows found by split-K slices (K = 1024) and by whole-K tiles
