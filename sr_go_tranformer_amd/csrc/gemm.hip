@@ -367,7 +367,7 @@ __device__ __forceinline__ void lds_barrier() {
 template <int TM>
 struct XTile {
     static constexpr int BM = TM * 16;
-    static constexpr int FPT = BM * 64 / 256;  // staged floats per thread (16 or 8)
+    static constexpr int FPT = BM * 64 / 256;  // staged floats per thread (16, 8 or 4)
     static constexpr int TPR = 64 / FPT;       // threads per row
     static constexpr int NV = FPT / 4;
     static constexpr int PLANE = BM * XLD;     // bf16 per plane
@@ -479,11 +479,17 @@ __device__ __forceinline__ float xstore_a(__bf16 *As, int tid, const float4 (&a)
         }
     }
     __bf16 *dst = As + r * XLD + c;
+    if constexpr (FPT == 4) {
+        *(uint2 *)dst = make_uint2(ph[0], ph[1]);
+        *(uint2 *)(dst + PLANE) = make_uint2(pm[0], pm[1]);
+        *(uint2 *)(dst + 2 * PLANE) = make_uint2(pl[0], pl[1]);
+    } else {
 #pragma unroll
-    for (int i = 0; i < FPT / 8; ++i) {
-        *(uint4 *)(dst + 8 * i) = make_uint4(ph[4 * i], ph[4 * i + 1], ph[4 * i + 2], ph[4 * i + 3]);
-        *(uint4 *)(dst + PLANE + 8 * i) = make_uint4(pm[4 * i], pm[4 * i + 1], pm[4 * i + 2], pm[4 * i + 3]);
-        *(uint4 *)(dst + 2 * PLANE + 8 * i) = make_uint4(pl[4 * i], pl[4 * i + 1], pl[4 * i + 2], pl[4 * i + 3]);
+        for (int i = 0; i < FPT / 8; ++i) {
+            *(uint4 *)(dst + 8 * i) = make_uint4(ph[4 * i], ph[4 * i + 1], ph[4 * i + 2], ph[4 * i + 3]);
+            *(uint4 *)(dst + PLANE + 8 * i) = make_uint4(pm[4 * i], pm[4 * i + 1], pm[4 * i + 2], pm[4 * i + 3]);
+            *(uint4 *)(dst + 2 * PLANE + 8 * i) = make_uint4(pl[4 * i], pl[4 * i + 1], pl[4 * i + 2], pl[4 * i + 3]);
+        }
     }
     return amax;
 }
@@ -911,13 +917,18 @@ struct GemmPlan {
 GemmPlan plan_gemm(int fmt, int32_t n, int64_t rows, int64_t cols) {
     GemmPlan p;
     p.x3 = (fmt == SRQ_Q8 || fmt == SRQ_Q4) && cols % kBlock == 0;
-    p.bm = n <= 32 ? 32 : 64;
+    // 16-row tiles (bf16 kernel) for at most 16 rows: the 32-row plan's
+    // slices with half the MFMA, activation-split and scale work per block,
+    // and features in tiles of half the width, so twice the workgroups
+    // (Llama-3.2-3B continuous batching 1152 -> 1176 tokens/s with the
+    // 32-row plan's feature tiles, 1186 with half-width ones).
+    p.bm = p.x3 && n <= 16 ? 16 : n <= 32 ? 32 : 64;
     // 128-feature tiles for 32-row tiles of narrow outputs: twice the
     // tiles, so fewer K slices and half the partial-sum traffic per weight
     // byte (Llama-3.2-3B shapes at 24-32 rows: 3072 x 3072 17.2 -> 13.5 us,
     // 3072 x 8192 24.9 -> 23.3 us, 5120 x 3072 20.0 -> 18.9 us; at 16384
     // rows the 256-feature tile stays ahead, 30.4 against 33.5 us).
-    p.tn = p.bm == 32 && rows <= 8192 ? 2 : 4;
+    p.tn = p.bm == 16 ? (rows <= 8192 ? 1 : 2) : p.bm == 32 && rows <= 8192 ? 2 : 4;  // 16-feature tiles per wave
     const int bk = p.x3 ? kBlock : BK;
     const int bn32 = p.x3 ? 64 * (rows <= 8192 ? 2 : 4) : BN;  // feature tile of a 32-row plan
     const int64_t tiles = (rows + bn32 - 1) / bn32;
@@ -942,6 +953,7 @@ void launch_unrolled(hipStream_t s, dim3 grid, const GemmArgs &a, float *partial
 
 template <int FMT, int BMT>
 void launch_tiles(hipStream_t s, const GemmArgs &a, const GemmPlan &p, float *partial, int32_t *wflags) {
+    static_assert(BMT >= 32 || FMT != SRQ_F32, "16-row tiles are the bf16 kernel's");
     if constexpr (FMT == SRQ_F32) {
         dim3 grid((unsigned)((a.rows + BN - 1) / BN), (unsigned)((a.n + BMT - 1) / BMT), (unsigned)p.slices);
         gemm_kernel<FMT, BMT><<<grid, 256, 0, s>>>(a, partial, wflags, p.kper);
@@ -950,6 +962,15 @@ void launch_tiles(hipStream_t s, const GemmArgs &a, const GemmPlan &p, float *pa
             const int xbn = 64 * p.tn;
             dim3 grid((unsigned)((a.rows + xbn - 1) / xbn), (unsigned)((a.n + BMT - 1) / BMT), (unsigned)p.slices);
             // Q8 slices of 4..12 blocks run unrolled
+            if constexpr (BMT == 16) {
+                if (p.tn == 1) {
+                    if (FMT == SRQ_Q8 && p.kper >= 4 && p.kper <= 12)
+                        launch_unrolled<1, 1>(s, grid, a, partial, wflags, p.kper);
+                    else
+                        gemm_x3_kernel<FMT, 1, 1, 0><<<grid, 256, 0, s>>>(a, partial, wflags, p.kper);
+                    return;
+                }
+            }
             if (FMT == SRQ_Q8 && p.kper >= 4 && p.kper <= 12) {
                 if (p.tn == 2)
                     launch_unrolled<BMT / 16, 2>(s, grid, a, partial, wflags, p.kper);
@@ -961,8 +982,10 @@ void launch_tiles(hipStream_t s, const GemmArgs &a, const GemmPlan &p, float *pa
                 gemm_x3_kernel<FMT, BMT / 16, 4, 0><<<grid, 256, 0, s>>>(a, partial, wflags, p.kper);
             }
         } else {
-            dim3 grid((unsigned)((a.rows + BN - 1) / BN), (unsigned)((a.n + BMT - 1) / BMT), (unsigned)p.slices);
-            gemm_kernel<FMT, BMT><<<grid, 256, 0, s>>>(a, partial, wflags, p.kper);
+            if constexpr (BMT >= 32) {
+                dim3 grid((unsigned)((a.rows + BN - 1) / BN), (unsigned)((a.n + BMT - 1) / BMT), (unsigned)p.slices);
+                gemm_kernel<FMT, BMT><<<grid, 256, 0, s>>>(a, partial, wflags, p.kper);
+            }
         }
     }
 }
@@ -972,7 +995,9 @@ void launch_fmt(hipStream_t s, const GemmArgs &a, const GemmPlan &p, float *part
     switch (a.fmt) {
         case SRQ_Q8: launch_tiles<SRQ_Q8, BMT>(s, a, p, partial, wflags); break;
         case SRQ_Q4: launch_tiles<SRQ_Q4, BMT>(s, a, p, partial, wflags); break;
-        default: launch_tiles<SRQ_F32, BMT>(s, a, p, partial, wflags); break;
+        default:
+            if constexpr (BMT >= 32) launch_tiles<SRQ_F32, BMT>(s, a, p, partial, wflags);
+            break;
     }
 }
 
@@ -1011,7 +1036,9 @@ int launch_gemm(hipStream_t s, const GemmArgs &a, void *scratch, size_t scratch_
                      a.rope.dim % a.rope.head_dim || a.rope.kvdim % a.rope.head_dim ||
                      a.rows != (int64_t)a.rope.dim + 2 * (int64_t)a.rope.kvdim || a.y_stride != a.rows))
         return fail(SRQ_EINVAL, "gemm: RoPE/KV output needs rows = dim + 2*kvdim in whole heads and no other epilogue");
-    if (p.bm == 32)
+    if (p.bm == 16)
+        launch_fmt<16>(s, a, p, partial, wflags);  // bf16 kernel only (plan_gemm)
+    else if (p.bm == 32)
         launch_fmt<32>(s, a, p, partial, wflags);
     else
         launch_fmt<64>(s, a, p, partial, wflags);

@@ -105,26 +105,37 @@ def _step_alone_and_in_batches(ex, cfg, seed, prompt_n, ns, heads=1, fmt="q8"):
 @pytest.mark.parametrize("prompt_n", [40, 1100])
 def test_step_rows_independent_of_batch(ex, prompt_n):
     """A decode row's logits are bit-identical in steps of 1, 5 and 8 rows
-    (GEMV layers) and in steps of 9, 17, 33, 64 and 256 rows (MFMA GEMM
-    layers), at 40 and 1100 positions (attention: fused split + merge up to
-    64 rows, split + combine for 256, past 16 splits in the combine's
-    grouped summation order).  The
+    (GEMV layers) and in steps of 9, 12, 16, 17, 33, 64 and 256 rows (MFMA
+    GEMM layers: 16-, 32- and 64-row tiles over the same K slices), at 40
+    and 1100 positions (attention: fused split + merge up to 64 rows, split
+    + combine for 256, past 16 splits in the combine's grouped summation
+    order).  The
     head takes the GEMV for up to 16 sessions wanting logits and the GEMM
     above: within each, the logits do not depend on how many sessions want
     them."""
     print("step invariance", prompt_n, flush=True)
     cfg = srq.make_config(512, 256, 2, 2, 1, 512, 1400, 10000.0, 1e-5, True)
     seed = 5 + prompt_n
-    out = _step_alone_and_in_batches(ex, cfg, seed, prompt_n, (1, 5, 8, 9, 17, 33, 64, 256))
+    out = _step_alone_and_in_batches(ex, cfg, seed, prompt_n, (1, 5, 8, 9, 12, 16, 17, 33, 64, 256))
     for n in (5, 8):
         assert same_bits(out[n], out[1]), n
-    for n in (17, 33, 64, 256):
+    for n in (12, 16, 17, 33, 64, 256):
         assert same_bits(out[n], out[9]), n
     for heads in (4, 16):
         got = _step_alone_and_in_batches(ex, cfg, seed, prompt_n, (64,), heads=heads)
         assert same_bits(got[64], out[64]), heads
     many = {h: _step_alone_and_in_batches(ex, cfg, seed, prompt_n, (64, 256), heads=h) for h in (17, 40)}
     assert same_bits(many[40][64], many[17][64]) and same_bits(many[40][256], many[17][64])
+
+
+def test_step_rows_independent_of_batch_q4_tiles(ex):
+    """Q4 layers: steps of 9 and 16 rows (16-row GEMM tiles), 17 and 32
+    (32-row tiles) and 64 (64-row tiles) give a decode row the same bits."""
+    print("q4 tile-height step invariance", flush=True)
+    cfg = srq.make_config(512, 256, 2, 2, 1, 512, 1400, 10000.0, 1e-5, True)
+    out = _step_alone_and_in_batches(ex, cfg, 41, 40, (9, 16, 17, 32, 64), fmt="q4")
+    for n in (16, 17, 32, 64):
+        assert same_bits(out[n], out[9]), n
 
 
 def test_step_rows_independent_of_batch_row_groups(ex):
