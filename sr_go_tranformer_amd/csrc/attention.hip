@@ -657,6 +657,97 @@ __device__ __forceinline__ void merge_one_head(const AttnArgs &A, const float *p
     }
 }
 
+// merge_one_head for a slice of the head's dims: workgroup z of
+// kMergeSlices takes dims [z*hd/kMergeSlices, +hd/kMergeSlices), so a head's
+// partial loads spread over that many CUs (one CU per head waited about 3 us
+// on its 68 KB of partials at 8k context).  Each workgroup forms M, l, lse
+// and the factors itself, one split's exps per thread; wave 0 folds l as
+// merge_one_head's lanes do (lane i: splits i, i+64, ... in order, then the
+// butterfly).  The same values in the same order, so the same bits.
+constexpr int kMergeSlices = 8;
+__device__ __forceinline__ void merge_one_head_slice(const AttnArgs &A, const float *part, int nsplit, int row, int h,
+                                                     int hd, int used, float *cf) {
+    __shared__ double terms[kMergeChunk];
+    __shared__ float wmax[4];
+    __shared__ double s_lse;
+    __shared__ float gs[256];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int ng = 256 / hd, per = (used + ng - 1) / ng;
+    const int dn = hd / kMergeSlices, d0 = (int)blockIdx.z * dn;
+    // chain threads: (dim d0 + tid % dn, group tid / dn), tid < dn * ng
+    const bool chain = tid < dn * ng;
+    const int j = d0 + tid % dn, q = tid / dn;
+    const int b0 = q * per, b1 = min(used, b0 + per), last = max(b1 - 1, 0);
+    const int64_t st = hd + 4;
+    const float *pb = partial((float *)part, row, h, 0, A.heads, nsplit, hd) + 4 + j;
+    constexpr int PRE = 4 * kMergeBatch;  // partials preloaded per chain thread
+    float vp[PRE], vq[kMergeBatch];         // the group's first PRE splits, then the next batch
+    if (chain) {
+#pragma unroll
+        for (int b = 0; b < PRE; ++b) vp[b] = pb[(int64_t)min(b0 + b, last) * st];
+#pragma unroll
+        for (int b = 0; b < kMergeBatch; ++b) vq[b] = pb[(int64_t)min(b0 + PRE + b, last) * st];
+    }
+    // split tid's {m, l}
+    float mt = -FLT_MAX;
+    double lt = 0.0;
+    if (tid < used) {
+        const float *p = partial((float *)part, row, h, tid, A.heads, nsplit, hd);
+        mt = p[0];
+        lt = *(const double *)(p + 2);
+    }
+    // butterflies by DPP / permlane (wave_max, wave_sum: a __shfl_xor
+    // butterfly's bits)
+    float M = wave_max(mt);
+    if (lane == 0) wmax[wave] = M;
+    __syncthreads();
+    M = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+    if (tid < used) terms[tid] = lt * exp((double)mt - (double)M);
+    __syncthreads();
+    if (wave == 0) {
+        double l = 0.0;
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+            if (lane + 64 * b < used) l += terms[lane + 64 * b];
+        l = wave_sum(l);
+        if (lane == 0) s_lse = (double)M + log(l);
+    }
+    __syncthreads();
+    if (tid < used) cf[tid] = (float)exp((double)mt - s_lse);
+    __syncthreads();
+    if (chain) {
+        // One FMA chain over [b0, b1) in split order (merge_range's).  The
+        // factors are read into registers ahead of the chain: read from LDS
+        // inside it, each FMA waited a full LDS latency (3 us for 64).
+        float c[PRE];
+#pragma unroll
+        for (int b = 0; b < PRE; ++b) c[b] = cf[min(b0 + b, used - 1)];
+        float o = 0.0f;
+#pragma unroll
+        for (int b = 0; b < PRE; ++b)
+            if (b0 + b < b1) o = __builtin_fmaf(c[b], vp[b], o);
+        for (int i0 = b0 + PRE; i0 < b1; i0 += kMergeBatch) {
+            float cc[kMergeBatch];
+#pragma unroll
+            for (int b = 0; b < kMergeBatch; ++b) cc[b] = cf[min(i0 + b, used - 1)];
+            if (i0 > b0 + PRE) {
+#pragma unroll
+                for (int b = 0; b < kMergeBatch; ++b) vq[b] = pb[(int64_t)min(i0 + b, last) * st];
+            }
+#pragma unroll
+            for (int b = 0; b < kMergeBatch; ++b)
+                if (i0 + b < b1) o = __builtin_fmaf(cc[b], vq[b], o);
+        }
+        gs[tid] = o;
+    }
+    __syncthreads();
+    if (tid < dn) {
+        float v = gs[tid];
+        for (int r = 1; r < ng; ++r) v += gs[r * dn + tid];
+        A.out[(int64_t)row * A.heads * hd + (int64_t)h * hd + d0 + tid] = v;
+    }
+}
+
 // Merge of split partials (m_i, l_i, o_i) for heads h0 .. h0+nh-1 of a row,
 // by all 256 threads of the workgroup:
 //   M = max_i m_i, l = sum_i l_i exp(m_i - M) (FP64), lse = M + log(l),
@@ -669,10 +760,16 @@ template <bool GROUPS>
 __device__ __forceinline__ void merge_splits(const AttnArgs &A, const float *part, int nsplit, int row, int h0,
                                              int nh, int hd, int used, float (*cf)[kMergeChunk], double *lse) {
     if constexpr (GROUPS) {
+        // Launched with kMergeSlices workgroups per head (gridDim.z): the
+        // sliced merge where it applies, else workgroup 0 merges alone.
         if (nh == 1 && used > kChainSplits && used <= kMergeChunk && hd <= 128 && 256 % hd == 0) {
-            merge_one_head(A, part, nsplit, row, h0, hd, used, cf[0]);
+            if (gridDim.z == kMergeSlices && hd % kMergeSlices == 0)
+                merge_one_head_slice(A, part, nsplit, row, h0, hd, used, cf[0]);
+            else if (blockIdx.z == 0)
+                merge_one_head(A, part, nsplit, row, h0, hd, used, cf[0]);
             return;
         }
+        if (blockIdx.z != 0) return;
     }
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     for (int g = wave; g < nh; g += 4) {
@@ -1072,7 +1169,7 @@ int launch_attention(hipStream_t s, const AttnArgs &a, float *scratch, int32_t *
         attn_split_kernel<<<grid, 256, 0, s>>>(a, scratch, nsplit);
     SRQ_HIP(hipGetLastError());
     if (a.n <= kGroupRows)
-        attn_combine_kernel<true><<<dim3(a.n, a.heads), 256, 0, s>>>(a, scratch, nsplit, kSplit);
+        attn_combine_kernel<true><<<dim3(a.n, a.heads, kMergeSlices), 256, 0, s>>>(a, scratch, nsplit, kSplit);
     else
         attn_combine_kernel<false><<<dim3(a.n, a.heads), 256, 0, s>>>(a, scratch, nsplit, kSplit);
     SRQ_HIP(hipGetLastError());

@@ -161,6 +161,41 @@ def test_step_rows_independent_of_batch_long_context(ex, fmt):
         assert same_bits(out[n], out[1]), n
 
 
+def test_long_row_fused_and_sliced_merge_same_bits(ex):
+    """A decode row at 1100 positions (18 splits) alone takes the fused
+    split + merge kernel; beside a row at 3200 positions the step has more
+    than 48 splits and takes split + combine, where the row's one-head merge
+    runs on 8 workgroups per head (slices of the head's dims).  The row's
+    logits are bit-identical, and match the oracle's."""
+    print("fused vs sliced merge", flush=True)
+    cfg = srq.make_config(512, 256, 2, 2, 1, 512, 3400, 10000.0, 1e-5, True)
+    m, norms = gpu_models.synthetic(ex, cfg, "q8", 53)
+    om = gpu_models.oracle_from_device(ex, m, cfg, norms)
+    rng = np.random.default_rng(53)
+    a_ids = [int(t) for t in rng.integers(0, cfg.vocab, size=1101)]
+    b_ids = [int(t) for t in rng.integers(0, cfg.vocab, size=3201)]
+    pool = m.pool(2 * (36 + 102) + 8)
+
+    def prefill(ids):
+        c = pool.cache((len(ids) + 32) // 32 + 1)
+        for lo in range(0, len(ids), 256):
+            m.step([c], [ids[lo:min(lo + 256, len(ids))]])
+        return c
+
+    ca = prefill(a_ids[:1100])
+    alone = m.step([ca], [[a_ids[1100]]])[0]
+    ca.close()
+    ca, cb = prefill(a_ids[:1100]), prefill(b_ids[:3200])
+    beside = m.step([ca, cb], [[a_ids[1100]], [b_ids[3200]]], want=[True, False])[0]
+    ca.close()
+    cb.close()
+    assert same_bits(alone, beside)
+    oc = om.new_cache()
+    for lo in range(0, 1100, 256):
+        om.step([oc], [a_ids[lo:min(lo + 256, 1100)]], workers=16)
+    near(alone, om.step([oc], [[a_ids[1100]]], workers=16)[0])
+
+
 def test_multi_session_long_context_steps(ex):
     """Six sessions past 1024 positions decode one token per step together
     (a 6-row step: fused attention over more than 16 splits); logits
