@@ -575,17 +575,24 @@ __device__ __forceinline__ float merge_range(const float *pb, int hd, const floa
 #pragma unroll
             for (int b = 0; b < kMergeBatch; ++b) vb[b] = pb[(int64_t)min(i1 + b, last) * st];
         }
+        // each batch's factors into registers before its FMAs (an LDS read
+        // inside the chain would cost every FMA an LDS latency)
+        float ca[kMergeBatch], cb[kMergeBatch];
+#pragma unroll
+        for (int b = 0; b < kMergeBatch; ++b) ca[b] = cf[min(i0 + b, last)];
 #pragma unroll
         for (int b = 0; b < kMergeBatch; ++b)
-            if (i0 + b < b1) o = __builtin_fmaf(cf[i0 + b], va[b], o);
+            if (i0 + b < b1) o = __builtin_fmaf(ca[b], va[b], o);
         if (i1 >= b1) break;
         if (i1 + kMergeBatch < b1) {
 #pragma unroll
             for (int b = 0; b < kMergeBatch; ++b) va[b] = pb[(int64_t)min(i1 + kMergeBatch + b, last) * st];
         }
 #pragma unroll
+        for (int b = 0; b < kMergeBatch; ++b) cb[b] = cf[min(i1 + b, last)];
+#pragma unroll
         for (int b = 0; b < kMergeBatch; ++b)
-            if (i1 + b < b1) o = __builtin_fmaf(cf[i1 + b], vb[b], o);
+            if (i1 + b < b1) o = __builtin_fmaf(cb[b], vb[b], o);
     }
     return o;
 }
