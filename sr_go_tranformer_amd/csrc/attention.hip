@@ -598,79 +598,15 @@ __device__ __forceinline__ float merge_range(const float *pb, int hd, const floa
 }
 
 // merge_splits for one head of a decode-sized step past kChainSplits splits
-// (at most kMergeChunk; head_dim 64 / 128): the same M, l, factors and
-// grouped FMA order, on the same 256 threads, with fewer memory round trips:
-// each thread issues its group's first 4*kMergeBatch partial loads before the
-// split maxima are combined, and wave 0 forms the factors from the {m, l}
-// it already holds.
-__device__ __forceinline__ void merge_one_head(const AttnArgs &A, const float *part, int nsplit, int row, int h,
-                                               int hd, int used, float *cf) {
-    __shared__ float gs[256];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int ng = 256 / hd, per = (used + ng - 1) / ng;
-    const int j = tid % hd, q = tid / hd;
-    // a group starting past the splits is empty (it re-reads split used-1
-    // and adds nothing)
-    const int b0 = q * per, b1 = min(used, b0 + per), last = b1 - 1;
-    const int64_t st = hd + 4;
-    const float *pb = partial((float *)part, row, h, 0, A.heads, nsplit, hd) + 4 + j;
-    constexpr int PRE = 4 * kMergeBatch;  // partials preloaded per thread
-    float vp[PRE];
-#pragma unroll
-    for (int b = 0; b < PRE; ++b) vp[b] = pb[(int64_t)min(b0 + b, last) * st];
-    if (wave == 0) {
-        float mv[4], M = -FLT_MAX;
-        double lv[4], l = 0.0;
-#pragma unroll
-        for (int b = 0; b < 4; ++b) {
-            const int i = lane + 64 * b;
-            mv[b] = -FLT_MAX;
-            lv[b] = 0.0;
-            if (i < used) {
-                const float *p = partial((float *)part, row, h, i, A.heads, nsplit, hd);
-                mv[b] = p[0];
-                lv[b] = *(const double *)(p + 2);
-            }
-        }
-#pragma unroll
-        for (int b = 0; b < 4; ++b) M = fmaxf(M, mv[b]);
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
-#pragma unroll
-        for (int b = 0; b < 4; ++b)
-            if (lane + 64 * b < used) l += lv[b] * exp((double)mv[b] - (double)M);
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) l += __shfl_xor(l, o, 64);
-        const double lse = (double)M + log(l);
-#pragma unroll
-        for (int b = 0; b < 4; ++b)
-            if (lane + 64 * b < used) cf[lane + 64 * b] = (float)exp((double)mv[b] - lse);
-    }
-    __syncthreads();
-    // thread (j, q): one FMA chain over splits [b0, b1) of dim j, in order
-    // (past the preloaded ones, as merge_range does)
-    float o = 0.0f;
-#pragma unroll
-    for (int b = 0; b < PRE; ++b)
-        if (b0 + b < b1) o = __builtin_fmaf(cf[b0 + b], vp[b], o);
-    o = merge_range(pb, hd, cf, b0 + PRE, b1, o);
-    // the groups' sums added in group order
-    gs[tid] = o;
-    __syncthreads();
-    if (q == 0) {
-        float v = gs[j];
-        for (int r = 1; r < ng; ++r) v += gs[r * hd + j];
-        A.out[(int64_t)row * A.heads * hd + (int64_t)h * hd + j] = v;
-    }
-}
-
-// merge_one_head for a slice of the head's dims: workgroup z of
-// kMergeSlices takes dims [z*hd/kMergeSlices, +hd/kMergeSlices), so a head's
-// partial loads spread over that many CUs (one CU per head waited about 3 us
-// on its 68 KB of partials at 8k context).  Each workgroup forms M, l, lse
-// and the factors itself, one split's exps per thread; wave 0 folds l as
-// merge_one_head's lanes do (lane i: splits i, i+64, ... in order, then the
-// butterfly).  The same values in the same order, so the same bits.
+// (at most kMergeChunk; head_dim a multiple of kMergeSlices dividing 256), on
+// a slice of the head's dims: workgroup z of kMergeSlices takes dims
+// [z*hd/kMergeSlices, +hd/kMergeSlices), so a head's partial loads spread over
+// that many CUs.  Each workgroup forms M, l, lse and the factors itself, one
+// split's exps per thread; wave 0 folds l as merge_splits' lanes do (lane i:
+// splits i, i+64, ... in order, then the butterfly).  Each chain thread
+// (dim, group) preloads its group's first 4*kMergeBatch partials and the next
+// kMergeBatch, and reads its factors into registers ahead of the FMA chain.
+// The same values in the same order as merge_splits, so the same bits.
 constexpr int kMergeSlices = 8;
 __device__ __forceinline__ void merge_one_head_slice(const AttnArgs &A, const float *part, int nsplit, int row, int h,
                                                      int hd, int used, float *cf) {
@@ -769,11 +705,9 @@ __device__ __forceinline__ void merge_splits(const AttnArgs &A, const float *par
     if constexpr (GROUPS) {
         // Launched with kMergeSlices workgroups per head (gridDim.z): the
         // sliced merge where it applies, else workgroup 0 merges alone.
-        if (nh == 1 && used > kChainSplits && used <= kMergeChunk && hd <= 128 && 256 % hd == 0) {
-            if (gridDim.z == kMergeSlices && hd % kMergeSlices == 0)
-                merge_one_head_slice(A, part, nsplit, row, h0, hd, used, cf[0]);
-            else if (blockIdx.z == 0)
-                merge_one_head(A, part, nsplit, row, h0, hd, used, cf[0]);
+        if (nh == 1 && used > kChainSplits && used <= kMergeChunk && hd <= 128 && 256 % hd == 0 &&
+            hd % kMergeSlices == 0 && gridDim.z == kMergeSlices) {
+            merge_one_head_slice(A, part, nsplit, row, h0, hd, used, cf[0]);
             return;
         }
         if (blockIdx.z != 0) return;
