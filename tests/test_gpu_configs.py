@@ -87,45 +87,69 @@ def test_resident_bytes_match_layout_receipts(ex):
         assert got == want, (shape, fmt, got, want)
 
 
-@pytest.mark.timeout(1200)
-def test_mistral7b_q8_greedy_256_tokens(ex):
-    """The headline workload at full size: Mistral-7B shape, Q8, seeded
-    N(0, 0.02) weights (the benchmark's seed), a 128-token random prompt
-    prefilled in one step, then 256 greedy tokens: the first from the
-    prefill's device argmax, 255 from graph replays."""
-    prompt_n, count = 128, 256
+def greedy_at_depth(ex, fmt, prompt_n, count, seed, step_rows=8):
+    """Mistral-7B shape at all 32 layers in `fmt`, seeded N(0, 0.02) weights
+    (the benchmark's seed), a prompt_n-token random prompt prefilled in one
+    step, then `count` greedy tokens: the first from the prefill's device
+    argmax, the rest from graph replays of the decoder, identical to the
+    oracle's inferHFIDs loop (M:1212-1238).  On a second cache the same
+    tokens go through one-row srq_step calls (the decode GEMV path), whose
+    logits at the prefill and the first `step_rows` decode steps are held to
+    1e-4 against the oracle's step (out.Logits, M:1225-1227)."""
     cfg = syn.shape_config("mistral-7b", prompt_n + count)
     t0 = time.time()
-    m, norms = gpu_models.synthetic(ex, cfg, "q8", seed=1)
-    prompt = syn.random_prompt(prompt_n, cfg.vocab, 1)
+    m, norms = gpu_models.synthetic(ex, cfg, fmt, seed=seed)
+    prompt = syn.random_prompt(prompt_n, cfg.vocab, seed)
     pages = (prompt_n + count + 31) // 32
     pool = m.pool(2 * pages)
     c = pool.cache(pages)
     got = m.generate_greedy(c, prompt, count, chunk=prompt_n)
-    assert c.pos == prompt_n + count - 1
+    assert len(got) == count and c.pos == prompt_n + count - 1
     c2 = pool.cache(pages)
-    first_logits = m.step([c2], [prompt])[0]
+    step_logits = [m.step([c2], [prompt])[0]]
+    for i in range(step_rows):
+        step_logits.append(m.step([c2], [[got[i]]])[0])
     c2.close()
     print("gpu done %.1f s" % (time.time() - t0), flush=True)
     om = gpu_models.oracle_from_device(ex, m, cfg, norms)
     oc = om.new_cache()
     nxt = om.step([oc], [prompt], workers=WORKERS)[0]
     print("oracle prefill done %.1f s" % (time.time() - t0), flush=True)
-    near(first_logits, nxt)
-    want, margins = [], []
+    margins, errs = [], []
     for i in range(count):
+        if i < len(step_logits):
+            errs.append(near(step_logits[i], nxt))
         best = oracle.argmax(nxt)
         assert best >= 0
         margins.append(margin(nxt))
-        want.append(best)
         assert got[i] == best, (i, got[i], best, margins[-1])
         if i + 1 < count:
             nxt = om.step([oc], [[best]], workers=WORKERS)[0]
         if i % 32 == 31:
             print("token %d/%d identical (%.1f s)" % (i + 1, count, time.time() - t0), flush=True)
-    print("256 greedy tokens identical; min top-2 margin %.4g" % min(margins), flush=True)
+    print("%s: %d greedy tokens identical; min top-2 margin %.4g; logits of the prefill and %d one-row decode "
+          "steps within %.3g" % (fmt, count, min(margins), step_rows, max(errs)), flush=True)
     oc.close()
     om.close()
+    c.close()
+    pool.close()
+    m.close()
+
+
+@pytest.mark.timeout(1200)
+def test_mistral7b_q8_greedy_256_tokens(ex):
+    """The headline workload at full size: Q8, 128-token prompt, 256 greedy
+    tokens, and 8 decode steps' logits at 32 layers."""
+    greedy_at_depth(ex, "q8", 128, 256, 1)
+
+
+@pytest.mark.timeout(1200)
+def test_mistral7b_q4mixed_greedy_128_tokens(ex):
+    """q4-mixed (Q4 layer matrices with the shared pair decode, Q8 embedding
+    and head) at all 32 layers: 128-token prompt in one chunk (the bf16x3
+    MFMA GEMM), 128 greedy tokens from the Q4 decode GEMVs, and 8 decode
+    steps' logits."""
+    greedy_at_depth(ex, "q4-mixed", 128, 128, 1)
 
 
 @pytest.mark.timeout(1200)
@@ -164,13 +188,13 @@ def test_mistral7b_width_q4mixed_chunked_prefill(ex):
     om.close()
 
 
-@pytest.mark.timeout(1200)
-def test_llama3b_width_continuous_batching(ex):
-    """Llama-3.2-3B width (3072 / 24:8 heads / 8192 / vocab 128256, tied) at
-    2 layers, Q8: the benchmark's 32 requests (prompt lengths U[64, 1024]
-    from its seed) scheduled tick by tick (budget 64, prefill chunk 16,
-    mixed chunk 1) for 80 steps; sessions whose prompt completes sample at
-    T 0.8, top-p 0.9, top-k off, no penalty, from RNG{seed + i}.
+def run_batching(ex, layers, lens, out_n, seed, steps=None):
+    """Llama-3.2-3B width (3072 / 24:8 heads / 8192 / vocab 128256, tied),
+    Q8, `layers` layers: one request per prompt length, admitted together
+    and scheduled tick by tick as Engine.run does (budget 64, prefill chunk
+    16, mixed chunk 1; TickPlanner); sessions whose prompt completes sample
+    at T 0.8, top-p 0.9, top-k off, no penalty, from RNG{seed + i}.  Runs
+    `steps` ticks, or (None) until every session holds out_n outputs.
 
     Each step's wanted logits are held to the oracle's step at 1e-4, and
     every draw of the device sampler to the oracle's sampleWithBlocked on
@@ -178,11 +202,10 @@ def test_llama3b_width_continuous_batching(ex):
     from the device's tokens.  A draw from the oracle's own logits is not a
     bar: at T 0.8 the top-p set holds thousands of candidates whose values
     lie ~1e-5 apart, so any 1e-4 difference reorders neighbours and moves
-    the candidate a draw lands on; its agreement rate is printed."""
-    seed, sessions_n, out_n, steps = 1, 32, 128, 80
-    r = syn.SplitMix64(seed)
-    lens = [64 + r.intn(1024 - 64 + 1) for _ in range(sessions_n)]
-    cfg = srq.make_config(128256, 3072, 2, 24, 8, 8192, max(lens) + out_n + 1, 500000.0, 1e-5, True)
+    the candidate a draw lands on; its agreement rate is printed.  Returns
+    (planner, tokens sampled, live-set sizes per tick)."""
+    sessions_n = len(lens)
+    cfg = srq.make_config(128256, 3072, layers, 24, 8, 8192, max(lens) + out_n + 1, 500000.0, 1e-5, True)
     t0 = time.time()
     m, norms = gpu_models.synthetic(ex, cfg, "q8", seed=seed)
     om = gpu_models.oracle_from_device(ex, m, cfg, norms)
@@ -194,9 +217,11 @@ def test_llama3b_width_continuous_batching(ex):
     orng = [oracle.RNG(seed + i) for i in range(sessions_n)]
     params = srq.Sampling(0.8, 0, 0.9, 1.0)
     tp = TickPlanner(prompts, out_n, 64, 16, 1)
-    sampled_total, worst, agree = 0, 0.0, 0
-    for step in range(steps):
+    sampled_total, worst, agree, live = 0, 0.0, 0, []
+    step = 0
+    while not tp.done() and (steps is None or step < steps):
         sessions, chunks, want = tp.plan()
+        live.append(len(sessions))
         got = m.step([caches[i] for i in sessions], chunks, want=want)
         dev = m.last_logits_ptr
         wl = om.step([ocaches[i] for i in sessions], chunks, want=want, workers=WORKERS)
@@ -221,11 +246,46 @@ def test_llama3b_width_continuous_batching(ex):
                 sampled[i] = oid
             sampled_total += len(sel)
         tp.commit(sampled)
-        if step % 10 == 9:
-            print("step %d: %d tokens sampled, max rel err %.3g (%.1f s)" % (step + 1, sampled_total, worst,
-                                                                            time.time() - t0), flush=True)
-    print("draws equal to the oracle's draw on its own logits: %d of %d" % (agree, sampled_total), flush=True)
-    assert sampled_total >= 50
+        step += 1
+        if step % 10 == 0:
+            print("step %d: %d live, %d tokens sampled, max rel err %.3g (%.1f s)" % (
+                step, live[-1], sampled_total, worst, time.time() - t0), flush=True)
+    print("%d ticks, %d tokens sampled, max rel err %.3g; draws equal to the oracle's draw on its own logits: "
+          "%d of %d" % (step, sampled_total, worst, agree, sampled_total), flush=True)
     for c in ocaches:
         c.close()
+    for c in caches:
+        c.close()
     om.close()
+    pool.close()
+    m.close()
+    return tp, sampled_total, live
+
+
+@pytest.mark.timeout(1200)
+def test_llama3b_width_continuous_batching(ex):
+    """The benchmark's 32 requests (prompt lengths U[64, 1024] from its
+    seed, 128 outputs each) at 2 layers for the first 80 ticks: long
+    prompts prefilled 16 rows per tick beside decoding sessions."""
+    seed = 1
+    r = syn.SplitMix64(seed)
+    lens = [64 + r.intn(1024 - 64 + 1) for _ in range(32)]
+    _, sampled, _ = run_batching(ex, 2, lens, 128, seed, steps=80)
+    assert sampled >= 50
+
+
+@pytest.mark.timeout(1200)
+def test_llama3b_continuous_batching_to_completion(ex):
+    """All 28 layers, 32 requests with prompt lengths U[8, 64] and 8 outputs
+    each, ticked until every session has finished: sessions leave the live
+    set as they reach max_tokens, so the rotation runs modulo a shrinking
+    count (Engine.run M:8370-8476, scheduleTokens M:8180-8210)."""
+    seed = 3
+    r = syn.SplitMix64(seed)
+    lens = [8 + r.intn(64 - 8 + 1) for _ in range(32)]
+    tp, sampled, live = run_batching(ex, 28, lens, 8, seed)
+    assert tp.done()
+    assert all(len(o) == 8 for o in tp.outputs)
+    assert sampled == 32 * 8
+    assert live[0] == 32 and live[-1] < 32 and sorted(live, reverse=True) == live
+    assert len(set(live)) > 2, live
