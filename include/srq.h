@@ -143,8 +143,11 @@ int srq_linear_enqueue(srq_exec *e, float *y, const float *x, const srq_weight *
  * nothing.  The GEMM path's split-K partial sums and wide-row flags go to a
  * fixed device array of SRQ_NOALLOC_SCRATCH_BYTES owned by the library (one
  * per GPU, held until the process ends) instead of the executor's
- * workspace; a call whose plan needs more is rejected with SRQ_EINVAL
- * before anything is enqueued.  Every call on one GPU shares that array and
+ * workspace.  A call whose plan needs more runs its rows in GEMM
+ * sub-batches that fit the array, with the same bits (a row's GEMM result
+ * does not depend on the rows beside it); with 64 MiB every n up to 1024
+ * fits, and a plan that could not fit 17 rows would be rejected with
+ * SRQ_EINVAL before anything is enqueued.  Every call on one GPU shares that array and
  * leaves its contents behind: calls that overlap on one GPU (executors or
  * streams not ordered against each other) race, so the caller orders them. */
 #define SRQ_NOALLOC_SCRATCH_BYTES (64u << 20)
@@ -277,7 +280,10 @@ int srq_argmax(srq_exec *e, const float *logits, int32_t rows, int32_t vocab, in
  * SRQ_ENONFINITE if a row holds a non-finite logit; SRQ_EINVAL if a row has
  * no candidate.  Masses are summed exactly in fixed point (2^-44 of the top
  * probability), so a draw can differ from the reference's f64 running sums
- * only when it falls within ~1e-12 of a candidate boundary. */
+ * only when it falls within ~1e-12 of a candidate boundary.  Device scratch:
+ * at most 64 MiB per executor (about 1 MiB per row of a 128256-id
+ * vocabulary); calls with more rows sample them in groups that fit, with
+ * the same ids and states. */
 typedef struct {
     double temperature;
     int32_t top_k;

@@ -589,17 +589,37 @@ int srq_linear_noalloc(srq_exec *e, float *y, const float *x, const srq_weight *
     const char *yb = (const char *)y, *xb = (const char *)x;
     if (yb < xb + (size_t)n * w->cols * 4 && xb < yb + (size_t)n * w->rows * 4)
         return fail(SRQ_EINVAL, "y overlaps x");
+    // The GEMM's scratch grows linearly with n and its K slices depend on
+    // the matrix alone, so a row's bits do not change when the rows run in
+    // sub-batches of more than kLinearGemmRows: a call whose scratch exceeds
+    // the array runs in the fewest such sub-batches that fit it (with 64 MiB
+    // every n up to 1024 fits: the plan needs at most 512 KiB per row).
+    const size_t cap = (size_t)SRQ_NOALLOC_SCRATCH_BYTES;
     const size_t need = linear_scratch_bytes(*w, n);
-    if (need > (size_t)SRQ_NOALLOC_SCRATCH_BYTES)
-        return fail(SRQ_EINVAL,
-                    "srq_linear_noalloc: %d rows of a %lld x %lld matrix need %zu bytes of scratch, above the "
-                    "fixed %zu (use srq_linear)",
-                    n, (long long)w->rows, (long long)w->cols, need, (size_t)SRQ_NOALLOC_SCRATCH_BYTES);
+    int32_t batches = 1;
+    if (need > cap) {
+        const size_t per_row = need / (size_t)n;
+        const int32_t fit = (int32_t)(cap / per_row);
+        batches = (n + fit - 1) / std::max<int32_t>(fit, 1);
+        if (fit <= kLinearGemmRows || n / batches <= kLinearGemmRows)
+            return fail(SRQ_EINVAL,
+                        "srq_linear_noalloc: a %lld x %lld matrix needs %zu bytes of scratch per row, above what "
+                        "the fixed %zu holds for %d rows (use srq_linear)",
+                        (long long)w->rows, (long long)w->cols, per_row, cap, kLinearGemmRows + 1);
+    }
     void *buf = g_noalloc_scratch[e->device];  // set when e's device was prepared
     if (!buf) return fail(SRQ_EDEVICE, "no-allocation scratch missing on device %d", e->device);
     DeviceGuard g(e->device);
-    return run_linear(e, e->ws, *w, x, n, y, w->rows, nullptr, 0.0, nullptr, kLinearGemmRows, buf,
-                      (size_t)SRQ_NOALLOC_SCRATCH_BYTES);
+    // Sub-batches of n / batches rows, the first n % batches one row more;
+    // each is ordered after the previous one on the stream, so they share
+    // the array.
+    for (int32_t b = 0, r0 = 0; b < batches; ++b) {
+        const int32_t cnt = n / batches + (b < n % batches ? 1 : 0);
+        SRQ_CHECK(run_linear(e, e->ws, *w, x + (int64_t)r0 * w->cols, cnt, y + (int64_t)r0 * w->rows, w->rows,
+                             nullptr, 0.0, nullptr, kLinearGemmRows, buf, cap));
+        r0 += cnt;
+    }
+    return SRQ_OK;
 }
 
 // ------------------------------------------------------------------- model

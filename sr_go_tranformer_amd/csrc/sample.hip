@@ -34,6 +34,7 @@
 // kept so far, so the buckets before the one holding it are kept whole and
 // the unfiltered histogram finds the same bucket.  A candidate's mass is
 // recomputed where it is needed (it is a pure function of its value).
+#include <algorithm>
 #include <cfloat>
 #include <climits>
 
@@ -51,6 +52,10 @@ constexpr int kMaxChunks = 64; // chunks per row (one wave scans their shares)
 constexpr int kChunkMax = 8192; // ids per chunk, at most
 constexpr int kRankSort = 128;  // gathered candidates sorted by rank, at most (8 threads each)
 constexpr double kFix = 17592186044416.0;  // 2^44: mass of probability 1
+// Device scratch of one launch group (ranges, histograms, ids in bucket
+// order: about 1 MiB per row of a 128256-id vocabulary); calls with more
+// rows run in groups that fit it.
+constexpr size_t kSampleScratchMax = (size_t)64 << 20;
 // The scans give each thread two buckets / two sorted candidates.
 static_assert(kBuckets == 2 * kST && kList == 2 * kST, "two entries per thread");
 static_assert(8 * kRankSort <= kST, "8 threads per ranked candidate");
@@ -842,7 +847,8 @@ void sample_plan(int32_t rows, int32_t vocab, int32_t &chunks, int32_t &chunk_le
     chunks = (vocab + chunk_len - 1) / chunk_len;
 }
 
-size_t sample_scratch_bytes(int32_t rows, int32_t vocab) {
+// Scratch of one launch over `rows` rows.
+static size_t plan_bytes(int32_t rows, int32_t vocab) {
     int32_t chunks, len;
     sample_plan(rows, vocab, chunks, len);
     return (size_t)rows * chunks *
@@ -850,32 +856,62 @@ size_t sample_scratch_bytes(int32_t rows, int32_t vocab) {
             (size_t)len * sizeof(int32_t));
 }
 
+// Rows per launch group: the most (a power of two up to 1024) whose scratch
+// fits kSampleScratchMax.  A row's draw is exact whatever the chunk plan, so
+// grouping changes no result.
+static int32_t group_rows(int32_t vocab) {
+    int32_t g = 1024;
+    while (g > 1 && plan_bytes(g, vocab) > kSampleScratchMax) g /= 2;
+    return g;
+}
+
+size_t sample_scratch_bytes(int32_t rows, int32_t vocab) {
+    const int32_t g = group_rows(vocab);
+    if (rows <= g) return plan_bytes(rows, vocab);
+    const int32_t tail = rows % g;
+    return std::max(plan_bytes(g, vocab), tail ? plan_bytes(tail, vocab) : (size_t)0);
+}
+
 int launch_sample(hipStream_t s, const SampleArgs &a0, void *scratch) {
     if (a0.rows <= 0) return SRQ_OK;
     const size_t lds = (size_t)((a0.vocab + 31) / 32) * 4;
     if (lds > 48 * 1024) return fail(SRQ_EINVAL, "sample: vocabulary of %d ids exceeds the history bitmap", a0.vocab);
-    SampleArgs a = a0;
-    sample_plan(a.rows, a.vocab, a.chunks, a.chunk_len);
-    if (a.chunks > kMaxChunks || a.chunk_len > kChunkMax)
-        return fail(SRQ_EINVAL, "sample: vocabulary of %d ids exceeds the chunk plan", a.vocab);
-    // [ranges: rows x chunks][masses: rows x chunks x 2048][counts: likewise]
-    // [offsets: likewise][ids in bucket order: rows x chunks x chunk_len]
-    const size_t nb = (size_t)a.rows * a.chunks * kBuckets;
-    a.range = (SampleRange *)scratch;
-    a.hmass = (unsigned long long *)(a.range + (size_t)a.rows * a.chunks);
-    a.hcount = (uint32_t *)(a.hmass + nb);
-    a.hoff = a.hcount + nb;
-    a.order = (int32_t *)(a.hoff + nb);
-    const size_t clds = (size_t)((a.chunk_len + 31) / 32) * 4;
-    const dim3 grid(a.chunks, a.rows);
-    sample_range_kernel<<<grid, kCT, a.repeat_penalty != 1.0 ? clds : 0, s>>>(a);
-    SRQ_HIP(hipGetLastError());
-    if (a.temperature != 0.0) {
-        sample_mass_kernel<<<grid, kCT, a.repeat_penalty != 1.0 ? clds : 0, s>>>(a);
+    const int32_t g = group_rows(a0.vocab);
+    for (int32_t r0 = 0; r0 < a0.rows; r0 += g) {
+        // Rows [r0, r0 + a.rows) of the call: every per-row pointer moves on.
+        SampleArgs a = a0;
+        a.rows = std::min(g, a0.rows - r0);
+        if (a0.row_ids)
+            a.row_ids = a0.row_ids + r0;
+        else
+            a.logits = a0.logits + (int64_t)r0 * a0.vocab;
+        if (a0.history) a.history = a0.history + (int64_t)r0 * a0.history_stride;
+        if (a0.history_len) a.history_len = a0.history_len + r0;
+        if (a0.blocked) a.blocked = a0.blocked + r0;
+        a.rng = a0.rng + r0;
+        a.ids = a0.ids + r0;
+        sample_plan(a.rows, a.vocab, a.chunks, a.chunk_len);
+        if (a.chunks > kMaxChunks || a.chunk_len > kChunkMax)
+            return fail(SRQ_EINVAL, "sample: vocabulary of %d ids exceeds the chunk plan", a.vocab);
+        // [ranges: rows x chunks][masses: rows x chunks x 2048][counts: likewise]
+        // [offsets: likewise][ids in bucket order: rows x chunks x chunk_len]
+        const size_t nb = (size_t)a.rows * a.chunks * kBuckets;
+        a.range = (SampleRange *)scratch;
+        a.hmass = (unsigned long long *)(a.range + (size_t)a.rows * a.chunks);
+        a.hcount = (uint32_t *)(a.hmass + nb);
+        a.hoff = a.hcount + nb;
+        a.order = (int32_t *)(a.hoff + nb);
+        const size_t clds = (size_t)((a.chunk_len + 31) / 32) * 4;
+        const dim3 grid(a.chunks, a.rows);
+        sample_range_kernel<<<grid, kCT, a.repeat_penalty != 1.0 ? clds : 0, s>>>(a);
+        SRQ_HIP(hipGetLastError());
+        if (a.temperature != 0.0) {
+            sample_mass_kernel<<<grid, kCT, a.repeat_penalty != 1.0 ? clds : 0, s>>>(a);
+            SRQ_HIP(hipGetLastError());
+        }
+        sample_kernel<<<a.rows, kST, a.repeat_penalty != 1.0 ? lds : 0, s>>>(a);
         SRQ_HIP(hipGetLastError());
     }
-    sample_kernel<<<a.rows, kST, a.repeat_penalty != 1.0 ? lds : 0, s>>>(a);
-    SRQ_HIP(hipGetLastError());
     return SRQ_OK;
 }
 

@@ -256,9 +256,10 @@ def test_qkv_bias_through_fused_rope_reduction(ex, dim, heads, kv_heads, fmt):
 def test_wide_rows_through_fused_reductions(ex):
     """A value projection scaled to ~1e34 makes the attention output exceed
     f32(MaxFloat32/(2*64*127)) (M:4346-4354), so the o projection of a
-    40-row step (split-K MFMA GEMM, residual and RMSNorm in its reduction)
-    computes those rows in FP64 (linearQ8WideInto, M:4356-4382).  Logits and
-    K/V rows against the oracle's step."""
+    40-row step (split-K MFMA GEMM, residual and RMSNorm in its reduction),
+    of a 4-row step and of a 1-row step (the streaming GEMV) computes those
+    rows in FP64 (linearQ8WideInto, M:4356-4382).  Logits and K/V rows
+    against the oracle's step."""
     cfg = srq.make_config(300, 512, 2, 4, 1, 512, 1400, 10000.0, 1e-5, True)
     m, norms = gpu_models.synthetic(ex, cfg, "q8", 21)
     kvdim = cfg.dim // cfg.heads * cfg.kv_heads
@@ -272,8 +273,10 @@ def test_wide_rows_through_fused_reductions(ex):
     want = om.step([oc], [ids[:40]])[0]
     assert np.all(np.isfinite(got))
     near(got, want)
-    # the next rows (a 5-row step: the streaming GEMV's FP64 pass)
-    near(m.step([c], [ids[40:]])[0], om.step([oc], [ids[40:]])[0])
+    # the next rows (a 4-row step, then one row: the streaming GEMV's FP64
+    # pass)
+    near(m.step([c], [ids[40:44]])[0], om.step([oc], [ids[40:44]])[0])
+    near(m.step([c], [ids[44:]])[0], om.step([oc], [ids[44:]])[0])
     # V rows of ~1e35: an entry near cancellation carries the f32 rounding of
     # its ~1e35 terms, so the bound is relative to the row's largest entry.
     for layer in range(cfg.layers):

@@ -96,6 +96,32 @@ def test_sample_continuous_batching_parameters(ex):
     assert np.array_equal(gst, wst)
 
 
+def test_sample_many_rows_run_in_groups(ex):
+    """A call with more rows than one launch group's scratch holds (64 rows
+    at a 128256-id vocabulary) samples them in groups: every id and state
+    equals the oracle's, with histories, blocked ids and row_ids, whose
+    per-row pointers move with each group."""
+    rng = np.random.default_rng(33)
+    rows, vocab = 90, 128256
+    logits = rng.normal(0, 1.0, size=(rows, vocab)).astype(np.float32)
+    logits[::3] = rng.normal(0, 4.0, size=((rows + 2) // 3, vocab)).astype(np.float32)
+    hist = [list(rng.integers(0, vocab, size=rng.integers(0, 20))) for _ in range(rows)]
+    blocked = np.where(np.arange(rows) % 2 == 0, rng.integers(0, vocab, size=rows), -1).astype(np.int32)
+    seeds = rng.integers(0, 2**63, size=rows, dtype=np.uint64)
+    for t, k, p, rp in [(0.8, 0, 0.9, 1.0), (0.7, 40, 0.95, 1.2)]:
+        got, gst = run(ex, logits, srq.Sampling(t, k, p, rp), seeds, hist, blocked)
+        want, wst = oracle_rows(logits, t, k, p, rp, seeds, hist, blocked)
+        assert np.array_equal(got, want), (t, k, p, rp)
+        assert np.array_equal(gst, wst)
+    buf = srq.DeviceBuffer.from_numpy(ex, logits)
+    sel = list(range(rows - 1, -1, -1))[:77]
+    st = seeds[:77].copy()
+    got = srq.sample(ex, buf.ptr, len(sel), vocab, srq.Sampling(0.8, 0, 0.9, 1.0), st, row_ids=sel)
+    want, wst = oracle_rows(logits[sel], 0.8, 0, 0.9, 1.0, seeds[:77])
+    assert np.array_equal(got, want)
+    assert np.array_equal(st, wst)
+
+
 def test_sample_draws_follow_the_distribution(ex):
     """Frequencies over many draws follow softmax(logits / T)."""
     logits = np.array([[2.0, 1.0, 0.0, -1.0, 1.0]], np.float32)
