@@ -44,8 +44,17 @@ extern "C" {
 #define SRQ_EFORMAT (-74)    /* archive metadata rejected (index, header,
                               * names, shapes, dtypes, extents)              */
 
+/* Both enums are int-sized.  Compiled as C++ they have int as a fixed
+ * underlying type, so a caller's out-of-range value (e.g. 7 from cgo) is a
+ * valid value of the type that the entry points then reject with
+ * SRQ_EINVAL, not undefined behaviour. */
+#ifdef __cplusplus
+typedef enum : int { SRQ_F32 = 0, SRQ_Q8 = 1, SRQ_Q4 = 2 } srq_format;
+typedef enum : int { SRQ_SRC_F32 = 0, SRQ_SRC_BF16 = 1, SRQ_SRC_F16 = 2 } srq_src_dtype;
+#else
 typedef enum { SRQ_F32 = 0, SRQ_Q8 = 1, SRQ_Q4 = 2 } srq_format;
 typedef enum { SRQ_SRC_F32 = 0, SRQ_SRC_BF16 = 1, SRQ_SRC_F16 = 2 } srq_src_dtype;
+#endif
 
 typedef struct srq_exec srq_exec;
 typedef struct srq_weight srq_weight;

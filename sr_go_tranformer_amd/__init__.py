@@ -16,7 +16,9 @@ import os
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libsrq.so")
+# SRQ_LIB names another build of the library (the host-sanitized one the CPU
+# tests load under the sanitizer runtime).
+LIB_PATH = os.environ.get("SRQ_LIB") or os.path.join(HERE, "libsrq.so")
 
 F32, Q8, Q4 = 0, 1, 2
 SRC_F32, SRC_BF16, SRC_F16 = 0, 1, 2

@@ -4,6 +4,7 @@ readHFConfig (monolith.go:253-386).  Cases follow the reference's own
 hf_loader_test.go (TestHFRejectTensorCorruption :149-213, TestUniqueJSON
 :230-237, TestHFRejectMetadata :112-148, TestHFArchiveAndConversion :80-110)
 plus the checks those leave open."""
+import ctypes as C
 import json
 import os
 import struct
@@ -329,3 +330,48 @@ def test_config_context_and_eos_list(tmp_path):
     write_json(os.path.join(d, "config.json"), ok)
     cfg, _ = hf.read_config(d)
     assert cfg.rope_llama3 == 1 and cfg.rope_original == 32 and cfg.rope_factor == 8.0
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_random_header_corruption_fails_cleanly(tmp_path, seed):
+    """Archive headers come from untrusted files: random byte edits,
+    truncations and insertions of the reference archive's header (and of its
+    8-byte length field and the index) each return SRQ_OK or one of the
+    archive error codes, never anything else.  Run under the
+    host-sanitized library (tests/test_sanitized_cpu.py), this also checks
+    the parser never reads or writes out of bounds."""
+    d = str(tmp_path)
+    header, payload = reference_archive(d, sharded=True)
+    path = os.path.join(d, "part.safetensors")
+    index = os.path.join(d, "model.safetensors.index.json")
+    raw = shard_bytes(header, payload)
+    raw_index = open(index, "rb").read()
+    hlen = struct.unpack("<Q", raw[:8])[0]
+    rng = np.random.default_rng(seed)
+    codes = {srq.OK, srq.EFORMAT, srq.EFILE, srq.EINVAL}
+    for trial in range(60):
+        buf = bytearray(raw)
+        idx = bytearray(raw_index)
+        kind = trial % 5
+        if kind == 0:  # flip bytes of the JSON header
+            for p in rng.integers(8, 8 + hlen, size=int(rng.integers(1, 6))):
+                buf[p] = int(rng.integers(0, 256))
+        elif kind == 1:  # cut the file short
+            del buf[int(rng.integers(0, 8 + hlen + 64)):]
+        elif kind == 2:  # insert bytes into the header
+            p = int(rng.integers(8, 8 + hlen))
+            buf[p:p] = bytes(rng.integers(0, 256, size=int(rng.integers(1, 40)), dtype=np.uint8))
+        elif kind == 3:  # a wrong header length
+            lengths = [0, 1, hlen - 1, hlen + 1, 1 << 40, (1 << 64) - 1]
+            buf[:8] = struct.pack("<Q", lengths[int(rng.integers(0, len(lengths)))])
+        else:  # corrupt the shard index instead
+            for p in rng.integers(0, len(idx), size=int(rng.integers(1, 6))):
+                idx[p] = int(rng.integers(0, 256))
+        with open(path, "wb") as f:
+            f.write(bytes(buf))
+        with open(index, "wb") as f:
+            f.write(bytes(idx))
+        size = C.c_int64()
+        cfg, _ = hf.read_config(d)
+        rc = srq.lib().srq_archive_check(C.byref(cfg), os.fsencode(d), C.byref(size))
+        assert rc in codes, (seed, trial, kind, rc)
