@@ -404,11 +404,12 @@ def bench_continuous_batching(srq, args):
     params = srq.Sampling(0.8, 0, 0.9, 1.0)
     tp = TickPlanner(prompts, out_n, budget, chunk, mixed)
     steps, rows_total = 0, 0
+    flag = C.c_int32(0) if args.cancel_flag else None  # a context that is never canceled
     ex.synchronize()
     t0 = time.perf_counter()
     while not tp.done():
         sessions, chunks, want = tp.plan()
-        dev = model.step([caches[i] for i in sessions], chunks, want=want, host=False)
+        dev = model.step([caches[i] for i in sessions], chunks, want=want, host=False, cancel=flag)
         rows_total += sum(len(c) for c in chunks)
         steps += 1
         sel = [k for k in range(len(sessions)) if want[k]]
@@ -433,10 +434,47 @@ def bench_continuous_batching(srq, args):
         "value": round(gen / dt, 1), "unit": "tokens/s", "n_gpus": 1, "higher_is_better": True, "dtype": "f32",
         "data": "synthetic",
         "config": {"workload": "Llama-3.2-3B shape, Q8, 32 requests, prompts U[64,1024], %d outputs each, "
-                               "budget 64 / chunk 16 / mixed 1, T 0.8 top-p 0.9" % out_n, "seed": args.seed},
+                               "budget 64 / chunk 16 / mixed 1, T 0.8 top-p 0.9" % out_n, "seed": args.seed,
+                   "cancel_flag": bool(args.cancel_flag)},
         "seconds": round(dt, 3), "steps": steps, "rows_processed": rows_total,
         "rows_per_s": round(rows_total / dt, 1), "ms_per_step": round(dt * 1e3 / steps, 3),
         "prompt_tokens": sum(lens), "generated_tokens": gen}), flush=True)
+    return 0
+
+
+def bench_step_decode(srq, args):
+    """Mistral-7B shape, Q8, batch 1: the 128-token prompt prefilled in one
+    step, then greedy decode one srq_step per token (logits on the device,
+    device argmax), as an engine drives it without the graph decoder;
+    --cancel-flag passes a flag that is never raised, so the step paces its
+    layers for cancellation."""
+    from sr_go_tranformer_amd import synthetic
+    ex = srq.Executor(0)
+    cfg = synthetic.shape_config("mistral-7b", PROMPT + args.warmup + args.steps + 2)
+    model = synthetic.build(ex, cfg, "q8", args.seed)
+    prompt = synthetic.random_prompt(PROMPT, cfg.vocab, args.seed)
+    pool = model.pool((PROMPT + args.warmup + args.steps + 2) // 32 + 2)
+    cache = pool.cache((PROMPT + args.warmup + args.steps + 2) // 32 + 1)
+    flag = C.c_int32(0) if args.cancel_flag else None
+    model.step([cache], [prompt], host=False, cancel=flag)
+    tok = int(model.argmax_last()[0])
+    for _ in range(args.warmup):
+        model.step([cache], [[tok]], host=False, cancel=flag)
+        tok = int(model.argmax_last()[0])
+    ex.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        model.step([cache], [[tok]], host=False, cancel=flag)
+        tok = int(model.argmax_last()[0])
+    ex.synchronize()
+    dt = time.perf_counter() - t0
+    print(json.dumps({
+        "metric": "Mistral-7B-shape Q8 decode tokens/s, one srq_step per token", "value": round(args.steps / dt, 2),
+        "unit": "tokens/s", "n_gpus": 1, "higher_is_better": True, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": "Mistral-7B shape, Q8, batch 1, 128-token prompt, %d untimed and %d timed greedy "
+                               "decode steps through srq_step + srq_argmax" % (args.warmup, args.steps),
+                   "seed": args.seed, "cancel_flag": bool(args.cancel_flag)},
+        "ms_per_step": round(dt * 1e3 / args.steps, 4)}), flush=True)
     return 0
 
 
@@ -597,7 +635,8 @@ def main():
                     choices=["mistral7b-q8-decode", "mistral7b-q4mixed-decode", "smollm2-q8-decode",
                              "llama1b-q8-gemv-sweep",
                              "mistral7b-q4mixed-prefill", "llama3b-q8-continuous-batching",
-                             "mistral7b-q8-longctx-decode", "mistral7b-bf16-archive-load"],
+                             "mistral7b-q8-longctx-decode", "mistral7b-bf16-archive-load",
+                             "mistral7b-q8-step-decode"],
                     help="workload; the default is the headline Mistral-7B Q8 decode")
     ap.add_argument("--prompt-tokens", type=int, default=2048, help="mistral7b-q4mixed-prefill: prompt length")
     ap.add_argument("--gen-tokens", type=int, default=128,
@@ -611,6 +650,9 @@ def main():
     ap.add_argument("--gemv-fmt", default="q8", choices=["q8", "q4"], help="--gemv-only: weight format")
     ap.add_argument("--archive-dir", default=None,
                     help="mistral7b-bf16-archive-load: where the temporary archive is written (default: TMPDIR)")
+    ap.add_argument("--cancel-flag", action="store_true",
+                    help="llama3b-q8-continuous-batching / mistral7b-q8-step-decode: pass every srq_step a "
+                         "cancel flag that stays 0 (the step then paces its layers for cancellation)")
     ap.add_argument("--eager", action="store_true",
                     help="launch each decode kernel directly instead of replaying the captured graph "
                          "(for kernel tracers that cannot follow graph launches)")
@@ -636,6 +678,8 @@ def main():
         return bench_q4mixed_prefill(srq, args)
     if args.config == "llama3b-q8-continuous-batching":
         return bench_continuous_batching(srq, args)
+    if args.config == "mistral7b-q8-step-decode":
+        return bench_step_decode(srq, args)
     if args.config == "mistral7b-q8-longctx-decode":
         return bench_longctx_decode(srq, args)
     if args.config == "mistral7b-bf16-archive-load":

@@ -260,8 +260,9 @@ int srq_cache_read(srq_exec *e, const srq_cache *c, int32_t layer, int32_t pos0,
  * logits are computed; unselected rows are zeroed (M:6438-6448).  Every
  * argument is validated before anything is mutated; positions are committed
  * only on success.  cancel (host, nullable) is polled as layers complete
- * (M:6213, M:6377): the host then stays at most two layers ahead of the
- * device, so a flag raised while the step runs stops it within two layers;
+ * (M:6213, M:6377): the host then stays at most eight layers ahead of the
+ * device (a progress event every four), so a flag raised while the step
+ * runs stops it within about 8 to 12 layers;
  * nonzero => SRQ_ECANCELED once the layers already queued have drained, no
  * positions committed.  Without a flag the step is queued whole.
  * logits_host (nullable) receives a host copy. */
