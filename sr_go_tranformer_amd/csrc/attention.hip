@@ -830,12 +830,25 @@ __global__ __launch_bounds__(256) void attn_fused_kernel(const AttnArgs A, float
     const int G = A.heads / A.kv_heads, used = (A.meta.pos[row] + kSplit) / kSplit;
     // Each wave's partial stores complete before the barrier, so the split
     // is counted only once all of them are visible device-wide.
+    //
+    // Ordering of the exchange.  Every value that crosses workgroups is an
+    // agent-scope atomic access: the partials are written with sc1 stores
+    // (written through L2 to the device's coherence point) and read with sc1
+    // loads (served from it), and the count is an agent-scope atomic.  The
+    // writer waits for its stores' completion (s_waitcnt 0) before the
+    // barrier that precedes its count, and the merger issues its loads only
+    // after the barrier that follows the count's result; both barriers are
+    // compiler barriers for memory operations.  An acq_rel count would add a
+    // whole-L2 write-back before it and an L2 invalidation after it, which
+    // only non-atomic data needs; measured, it cost 0.3% of 7B decode at 150
+    // positions and 1.8% at 2k.
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     int32_t *cnt = counters + (int64_t)row * A.kv_heads + kh;
     if (tid == 0) last = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == used - 1;
     __syncthreads();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);  // no load of the merge moves above the count
     if (!last) return;
     if (tid == 0) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     // one wave per head merges on its own
