@@ -26,6 +26,7 @@
 //    linearQ4WideInto, M:4356-4382, M:4754-4780): by the workgroup itself
 //    when it saw all of K, else by the reduction from per-slice flags.
 #include <algorithm>
+#include <utility>
 
 #include "srq_internal.h"
 
@@ -494,6 +495,59 @@ __device__ __forceinline__ float xstore_a(__bf16 *As, int tid, const float4 (&a)
     return amax;
 }
 
+// Stores a tile's accumulators: partial sums of its K slice (partial !=
+// nullptr), else y (+ residual), rows holding a |x| > kWideLimit recomputed
+// in FP64.  D layout of 16x16x32: lane holds rows 4*(lane/16)+r, column
+// lane%16.
+template <int TM, int TN>
+__device__ __forceinline__ void x3_finish(const GemmArgs &G, float *__restrict__ partial, int32_t *__restrict__ wflags,
+                                          const floatx4 (&acc)[TM][TN], const float amax, int *row_wide,
+                                          const int64_t n0, const int64_t m0, const int tid) {
+    constexpr int BM = XTile<TM>::BM, XBN = 64 * TN;
+    const int lane = tid & 63, li = lane & 15, q = lane >> 4;
+    if (amax > kWideLimit) row_wide[tid / XTile<TM>::TPR] = 1;
+    lds_barrier();
+
+    if (partial) {
+        float *P = partial + (int64_t)blockIdx.z * G.n * G.rows;
+        if (blockIdx.x == 0 && tid < BM && m0 + tid < G.n) wflags[(int64_t)blockIdx.z * G.n + m0 + tid] = row_wide[tid];
+#pragma unroll
+        for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int64_t m = m0 + tm * 16 + 4 * q + r;
+                if (m >= G.n) continue;
+#pragma unroll
+                for (int tn = 0; tn < TN; ++tn) {
+                    const int64_t j = n0 + tn * 16 + li;
+                    if (j < G.rows) P[m * G.rows + j] = acc[tm][tn][r];
+                }
+            }
+        return;
+    }
+#pragma unroll
+    for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int mi = tm * 16 + 4 * q + r;
+            const int64_t m = m0 + mi;
+            if (m >= G.n || row_wide[mi]) continue;
+#pragma unroll
+            for (int tn = 0; tn < TN; ++tn) {
+                const int64_t j = n0 + tn * 16 + li;
+                if (j >= G.rows) continue;
+                float v = acc[tm][tn][r];
+                if (G.residual) v = G.residual[m * G.y_stride + j] + v;
+                G.y[m * G.y_stride + j] = v;
+            }
+        }
+    for (int mi = 0; mi < BM; ++mi) {
+        if (!row_wide[mi] || m0 + mi >= G.n) continue;
+        const int64_t j = (int64_t)blockIdx.x * XBN + tid;
+        if (tid < XBN && j < G.rows) G.y[(m0 + mi) * G.y_stride + j] = wide_output(G, m0 + mi, j);
+    }
+}
+
 // As gemm_kernel, for Q8 / Q4 weights and cols % 64 == 0; kper counts
 // 64-input blocks.
 //
@@ -690,48 +744,236 @@ __global__ __launch_bounds__(256, 2) void gemm_x3_kernel(const GemmArgs G, float
 #undef SRQ_LOAD_B
 #undef SRQ_LOAD_A
 #undef SRQ_CONVERT
-    if (amax > kWideLimit) row_wide[tid / XTile<TM>::TPR] = 1;
-    lds_barrier();
+    x3_finish<TM, TN>(G, partial, wflags, acc, amax, row_wide, n0, m0, tid);
+}
 
-    // D layout of 16x16x32: lane holds rows 4*(lane/16)+r, column lane%16.
-    if (partial) {
-        float *P = partial + (int64_t)blockIdx.z * G.n * G.rows;
-        if (blockIdx.x == 0 && tid < BM && m0 + tid < G.n) wflags[(int64_t)blockIdx.z * G.n + m0 + tid] = row_wide[tid];
+// Q8 operands read as whole 128-byte row segments (steps of 9-32 rows).
+//
+// gemm_x3_kernel loads each lane's MFMA operand straight from memory: one
+// wave instruction reads 16 bytes for each of 16 feature rows x 4 K
+// quarters, i.e. one 64-byte block of 16 rows, half of each of 16 cache
+// lines.  Streamed alone, that pattern moves 16384 x 3072 int8 in 15.0 us
+// against 9.3 us for an instruction reading 4 rows x 256 bytes (loads-only
+// kernel, 256 workgroups of 8 waves, 8 loads in flight per lane): the
+// memory path is bound by cache lines per instruction, not bytes.  Here a
+// wave reads a pair of blocks (two 64-input blocks, 128 bytes of a row) of
+// its 16 feature rows as two instructions of 8 rows x 128 bytes, stages
+// them in its own LDS region and reads each block back in the operand
+// layout.  A slice starting or ending on an odd block loads that block
+// alone, the old way.  Operands, MFMA order and the scale chain are those
+// of gemm_x3_kernel, so every output has the same bits.
+//
+// Region layout per 16-row tile: row r (0..15) holds its eight 16-byte
+// chunks at slots chunk ^ (r % 8) ^ (r / 8), so that both the stores (8
+// lanes per row) and the operand reads (16 rows per K quarter) touch
+// distinct banks.
+template <int KU, int ODD>
+struct PairRole {
+    // Block k of a slice of KU blocks whose first block has the parity ODD:
+    // first(k) loads blocks k and k + 1, single(k) loads block k alone.
+    static constexpr bool first(int k) { return (k + ODD) % 2 == 0 && k + 1 < KU; }
+    static constexpr bool single(int k) { return (k + ODD) % 2 == 0 ? k + 1 == KU : k == 0; }
+};
+
+// f(integral_constant<int, i>) for i = 0, 1, ... in order, as straight-line code.
+template <typename F, int... I>
+__device__ __forceinline__ void unroll_each(F &&f, std::integer_sequence<int, I...>) {
+    (f(std::integral_constant<int, I>{}), ...);
+}
+
+template <int TM, int TN, int KU, int DIST, int ODD>
+__device__ __forceinline__ void x3p_slice(const GemmArgs &G, const int64_t n0, const int64_t m0, const int gbeg,
+                                          const int gend, const int tid, __bf16 (*As)[3 * XTile<TM>::PLANE],
+                                          u32x4v *ws, float *ss, floatx4 (&acc)[TM][TN], float &amax) {
+    typedef PairRole<KU, ODD> Role;
+    constexpr int NV = XTile<TM>::NV, PLANE = XTile<TM>::PLANE, FPT = XTile<TM>::FPT, TPR = XTile<TM>::TPR;
+    // Activations run one block further ahead than weights and each
+    // block issues them first.  The wave's load counter retires in issue
+    // order, so a wait for block k+1's activations then never waits for
+    // weights of a block beyond k, and the weight loads keep DIST blocks in
+    // flight.
+    constexpr int DA = DIST + 1;
+    const int lane = tid & 63, li = lane & 15, q = lane >> 4;
+    const int64_t cols = G.cols, groups = cols / kBlock;
+    const int glast = gend - 1;
+    // 32-bit offsets from the matrix base (rows * cols < 2^32): one
+    // register per address instead of two
+    const uint8_t *__restrict__ W = (const uint8_t *)G.values;
+    uint32_t wo[TN], po[TN][2];
 #pragma unroll
-        for (int tm = 0; tm < TM; ++tm)
+    for (int tn = 0; tn < TN; ++tn) {
+        const int64_t row = n0 + tn * 16 + li;
+        const int64_t rc = row < G.rows ? row : G.rows - 1;
+        wo[tn] = (uint32_t)(rc * cols + 16 * q);
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int64_t m = m0 + tm * 16 + 4 * q + r;
-                if (m >= G.n) continue;
-#pragma unroll
-                for (int tn = 0; tn < TN; ++tn) {
-                    const int64_t j = n0 + tn * 16 + li;
-                    if (j < G.rows) P[m * G.rows + j] = acc[tm][tn][r];
-                }
-            }
-        return;
+        for (int i = 0; i < 2; ++i) {
+            const int64_t prow = n0 + tn * 16 + 8 * i + (lane >> 3);
+            const int64_t prc = prow < G.rows ? prow : G.rows - 1;
+            po[tn][i] = (uint32_t)(prc * cols + 16 * (lane & 7));
+        }
     }
+    // region slots: stores of row 8i + lane/8, chunk lane%8; operand reads of row li
+    const int wslot[2] = {(lane >> 3) * 8 + ((lane & 7) ^ (lane >> 3)), 64 + (lane >> 3) * 8 + ((lane & 7) ^ (lane >> 3) ^ 1)};
+    const int rsw = (li & 7) ^ (li >> 3);
+    const int64_t am = min(m0 + tid / TPR, (int64_t)G.n - 1);
+    const float *ap = G.x + am * cols + (tid % TPR) * FPT;
+
+    u32x4v praw[KU][TN][2], sraw[KU][TN];
+    float4 areg[DA][NV];
+    // The slice's scales of the workgroup's rows, loaded once in row order
+    // (KU consecutive floats per row, the lanes of an instruction spanning
+    // a few rows) into ss[row][block] (row stride KS, odd: the 16 rows of
+    // an operand read hit distinct banks).  Per-block scale loads of 16
+    // rows each would cost as many cache-line requests as the weights.
+    constexpr int XBN = 64 * TN, KS = KU | 1, SE = (XBN * KU + 255) / 256;
+    const int64_t wrow0 = n0 - (tid >> 6) * 16 * TN;  // the workgroup's first output
+    float sreg[SE];
 #pragma unroll
-    for (int tm = 0; tm < TM; ++tm)
+    for (int i = 0; i < SE; ++i) {
+        const int e = tid + 256 * i;
+        const int r = e / KU, j = e - r * KU;
+        const int64_t row = min(wrow0 + r, G.rows - 1);
+        // a block past the slice's end (last slice) is added with a zero scale
+        sreg[i] = e < XBN * KU && gbeg + j < gend ? G.scales[row * groups + min(gbeg + j, glast)] : 0.0f;
+    }
+    auto stage_s = [&]() {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int mi = tm * 16 + 4 * q + r;
-            const int64_t m = m0 + mi;
-            if (m >= G.n || row_wide[mi]) continue;
+        for (int i = 0; i < SE; ++i) {
+            const int e = tid + 256 * i;
+            const int r = e / KU, j = e - r * KU;
+            if (e < XBN * KU) ss[r * KS + j] = sreg[i];
+        }
+    };
+    const float *sl = ss + ((tid >> 6) * 16 * TN + li) * KS;  // this lane's rows
+    // Weight loads of block j (its scale, and its pair or its lone block).
+    // A phantom block past the slice's end (last slice) reads clamped,
+    // in-row data and is added with a zero scale.
+    auto load_w = [&](auto J) {
+        constexpr int j = decltype(J)::value;
+        if constexpr (j < KU) {
+            const int g = gbeg + j;
+            if constexpr (Role::first(j)) {
+                const uint32_t pg = (uint32_t)min((int64_t)g, groups - 2) * kBlock;
 #pragma unroll
-            for (int tn = 0; tn < TN; ++tn) {
-                const int64_t j = n0 + tn * 16 + li;
-                if (j >= G.rows) continue;
-                float v = acc[tm][tn][r];
-                if (G.residual) v = G.residual[m * G.y_stride + j] + v;
-                G.y[m * G.y_stride + j] = v;
+                for (int tn = 0; tn < TN; ++tn)
+#pragma unroll
+                    for (int i = 0; i < 2; ++i) praw[j][tn][i] = *(const u32x4v *)(W + (uint64_t)(po[tn][i] + pg));
+            } else if constexpr (Role::single(j)) {
+                const uint32_t sg = (uint32_t)min(g, glast) * kBlock;
+#pragma unroll
+                for (int tn = 0; tn < TN; ++tn) sraw[j][tn] = *(const u32x4v *)(W + (uint64_t)(wo[tn] + sg));
             }
         }
-    for (int mi = 0; mi < BM; ++mi) {
-        if (!row_wide[mi] || m0 + mi >= G.n) continue;
-        const int64_t j = (int64_t)blockIdx.x * XBN + tid;
-        if (tid < XBN && j < G.rows) G.y[(m0 + mi) * G.y_stride + j] = wide_output(G, m0 + mi, j);
-    }
+    };
+    auto load_a = [&](auto J) {
+        constexpr int j = decltype(J)::value;
+        if constexpr (j < KU) {
+            const int64_t g = min(gbeg + j, glast);
+#pragma unroll
+            for (int i = 0; i < NV; ++i) areg[j % DA][i] = *(const float4 *)(ap + g * kBlock + 4 * i);
+        }
+    };
+    auto stage_w = [&](auto J) {
+        constexpr int j = decltype(J)::value;
+#pragma unroll
+        for (int tn = 0; tn < TN; ++tn)
+#pragma unroll
+            for (int i = 0; i < 2; ++i) ws[tn * 128 + wslot[i]] = praw[j][tn][i];
+    };
+
+    // issue order A0, A1, W0, A2, W1, ..., A(DA-1), W(DIST-1): each
+    // block's weights after the activations one block further on
+    load_a(std::integral_constant<int, 0>{});
+    unroll_each([&](auto J) {
+        constexpr int j = decltype(J)::value;
+        load_a(std::integral_constant<int, j + 1>{});
+        load_w(J);
+    }, std::make_integer_sequence<int, DIST>{});
+    stage_s();
+    if constexpr (Role::first(0)) stage_w(std::integral_constant<int, 0>{});
+    amax = xstore_a<TM>(As[0], tid, areg[0]);
+    lds_barrier();
+
+    unroll_each([&](auto K) {
+        constexpr int k = decltype(K)::value;
+        constexpr int u = k & 1, v = u ^ 1;
+        bf16x8 b[TN][2];
+        if constexpr (Role::single(k)) {
+#pragma unroll
+            for (int tn = 0; tn < TN; ++tn) xcodes<SRQ_Q8>(sraw[k][tn], b[tn][0], b[tn][1]);
+        } else {
+            constexpr int half = Role::first(k) ? 0 : 1;
+#pragma unroll
+            for (int tn = 0; tn < TN; ++tn)
+                xcodes<SRQ_Q8>(ws[tn * 128 + li * 8 + ((4 * half + q) ^ rsw)], b[tn][0], b[tn][1]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        load_a(std::integral_constant<int, k + DA>{});
+        load_w(std::integral_constant<int, k + DIST>{});
+        __builtin_amdgcn_sched_barrier(0);
+        const __bf16 *as = As[u];
+#pragma unroll
+        for (int tm = 0; tm < TM; ++tm) {
+            bf16x8 a[3][2];
+#pragma unroll
+            for (int t = 0; t < 3; ++t)
+#pragma unroll
+                for (int h = 0; h < 2; ++h)
+                    a[t][h] = *(const bf16x8 *)(as + t * PLANE + (tm * 16 + li) * XLD + 16 * q + 8 * h);
+#pragma unroll
+            for (int tn = 0; tn < TN; ++tn) {
+                floatx4 blk = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int t = 2; t >= 0; --t)
+#pragma unroll
+                    for (int h = 0; h < 2; ++h)
+                        blk = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[t][h], b[tn][h], blk, 0, 0, 0);
+                const float sc_u = sl[tn * 16 * KS + k];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) acc[tm][tn][r] = __builtin_fmaf(blk[r], sc_u, acc[tm][tn][r]);
+            }
+        }
+        if constexpr (k + 1 < KU) {
+            // the next pair -> the region (after this block's reads of it),
+            // block k+1's activations -> the other stage
+            if constexpr (Role::first(k + 1)) stage_w(std::integral_constant<int, k + 1>{});
+            amax = fmaxf(amax, xstore_a<TM>(As[v], tid, areg[(k + 1) % DA]));
+            lds_barrier();
+        }
+    }, std::make_integer_sequence<int, KU>{});
+}
+
+// Q8, 16- or 32-row tiles, cols % 128 == 0, rows * cols < 2^32, slices of exactly KU blocks
+// (the last slice may be shorter).  DIST: blocks between a block's loads
+// and its use.
+// Four feature tiles per wave need more than the 256 registers of two
+// workgroups per CU; their grids (outputs above 8192) hold about one
+// workgroup per CU anyway.
+template <int TM, int TN, int KU, int DIST>
+__global__ __launch_bounds__(256, TN == 4 ? 1 : 2) void gemm_x3p_kernel(const GemmArgs G, float *__restrict__ partial,
+                                                          int32_t *__restrict__ wflags, const int kper) {
+    constexpr int BM = XTile<TM>::BM, PLANE = XTile<TM>::PLANE, XBN = 64 * TN;
+    __shared__ __attribute__((aligned(16))) __bf16 As[2][3 * PLANE];
+    __shared__ u32x4v Ws[4][TN * 128];
+    __shared__ float Ss[64 * TN * (KU | 1)];
+    __shared__ int row_wide[BM];
+    const int tid = threadIdx.x, wave = tid >> 6;
+    const int64_t n0 = (int64_t)blockIdx.x * XBN + wave * 16 * TN, m0 = (int64_t)blockIdx.y * BM;
+    const int groups = (int)(G.cols / kBlock);
+    const int gbeg = (int)blockIdx.z * kper;
+    const int gend = min(gbeg + kper, groups);
+    if (tid < BM) row_wide[tid] = 0;
+    floatx4 acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+    float amax = 0.0f;
+    if (gbeg & 1)
+        x3p_slice<TM, TN, KU, DIST, 1>(G, n0, m0, gbeg, gend, tid, As, Ws[wave], Ss, acc, amax);
+    else
+        x3p_slice<TM, TN, KU, DIST, 0>(G, n0, m0, gbeg, gend, tid, As, Ws[wave], Ss, acc, amax);
+    x3_finish<TM, TN>(G, partial, wflags, acc, amax, row_wide, n0, m0, tid);
 }
 
 // The same for four consecutive outputs (rows, y_stride and the plane are
@@ -951,6 +1193,21 @@ void launch_unrolled(hipStream_t s, dim3 grid, const GemmArgs &a, float *partial
     }
 }
 
+// Pair-streamed Q8 tiles (gemm_x3p_kernel): blocks between a block's
+// weight loads and its MFMAs.
+template <int TN>
+constexpr int kPairDist = 4;
+
+template <int TM, int TN, int KU = 4>
+void launch_pairs(hipStream_t s, dim3 grid, const GemmArgs &a, float *partial, int32_t *wflags, int kper) {
+    if constexpr (KU <= 12) {
+        if (kper == KU)
+            gemm_x3p_kernel<TM, TN, KU, kPairDist<TN>><<<grid, 256, 0, s>>>(a, partial, wflags, kper);
+        else
+            launch_pairs<TM, TN, KU + 1>(s, grid, a, partial, wflags, kper);
+    }
+}
+
 template <int FMT, int BMT>
 void launch_tiles(hipStream_t s, const GemmArgs &a, const GemmPlan &p, float *partial, int32_t *wflags) {
     static_assert(BMT >= 32 || FMT != SRQ_F32, "16-row tiles are the bf16 kernel's");
@@ -961,7 +1218,20 @@ void launch_tiles(hipStream_t s, const GemmArgs &a, const GemmPlan &p, float *pa
         if (p.x3) {
             const int xbn = 64 * p.tn;
             dim3 grid((unsigned)((a.rows + xbn - 1) / xbn), (unsigned)((a.n + BMT - 1) / BMT), (unsigned)p.slices);
-            // Q8 slices of 4..12 blocks run unrolled
+            // Q8 slices of 4..12 blocks run unrolled; at 16 and 32 rows with
+            // whole 128-byte row segments (cols % 128 == 0), pair-streamed
+            if constexpr (BMT <= 32) {
+                if (FMT == SRQ_Q8 && p.kper >= 4 && p.kper <= 12 && a.cols % (2 * kBlock) == 0 &&
+                    (uint64_t)a.rows * (uint64_t)a.cols <= UINT32_MAX) {
+                    if (p.tn == 1)
+                        launch_pairs<BMT / 16, 1>(s, grid, a, partial, wflags, p.kper);
+                    else if (p.tn == 2)
+                        launch_pairs<BMT / 16, 2>(s, grid, a, partial, wflags, p.kper);
+                    else if constexpr (BMT == 32)  // 16-row plans take at most 2 tiles
+                        launch_pairs<2, 4>(s, grid, a, partial, wflags, p.kper);
+                    return;
+                }
+            }
             if constexpr (BMT == 16) {
                 if (p.tn == 1) {
                     if (FMT == SRQ_Q8 && p.kper >= 4 && p.kper <= 12)
