@@ -252,7 +252,7 @@ def bench_smollm2(srq, args):
         cache = pool.cache(4)
         model.step([cache], [prompt])
         first = int(model.argmax_last()[0])
-        dec = srq.Decoder(model, cache, first, 63)
+        dec = srq.Decoder(model, cache, first, 63, eager=args.eager)
         ex.synchronize()
         a, b = hip.create(), hip.create()
         hip.record(a, stream)

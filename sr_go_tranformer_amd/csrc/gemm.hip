@@ -365,13 +365,14 @@ __device__ __forceinline__ void lds_barrier() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
-template <int TM>
+template <int TM, int NT = 256>
 struct XTile {
     static constexpr int BM = TM * 16;
-    static constexpr int FPT = BM * 64 / 256;  // staged floats per thread (16, 8 or 4)
-    static constexpr int TPR = 64 / FPT;       // threads per row
+    static constexpr int FPT = BM * 64 / NT;  // staged floats per thread (16, 8 or 4)
+    static constexpr int TPR = 64 / FPT;      // threads per row
     static constexpr int NV = FPT / 4;
-    static constexpr int PLANE = BM * XLD;     // bf16 per plane
+    static constexpr int PLANE = BM * XLD;    // bf16 per plane
+    static_assert(FPT >= 4, "at least one float4 per thread");
 };
 
 __device__ __forceinline__ uint32_t pk_hi16(float lo, float hi) {
@@ -456,9 +457,10 @@ __device__ __forceinline__ void xload_a(const float *__restrict__ X, int32_t n, 
 }
 
 // Splits the staged floats into the hi / mid / lo planes; returns max |x|.
-template <int TM>
-__device__ __forceinline__ float xstore_a(__bf16 *As, int tid, const float4 (&a)[XTile<TM>::NV]) {
-    constexpr int FPT = XTile<TM>::FPT, TPR = XTile<TM>::TPR, NV = XTile<TM>::NV, PLANE = XTile<TM>::PLANE;
+template <int TM, int NT = 256>
+__device__ __forceinline__ float xstore_a(__bf16 *As, int tid, const float4 (&a)[XTile<TM, NT>::NV]) {
+    typedef XTile<TM, NT> X;
+    constexpr int FPT = X::FPT, TPR = X::TPR, NV = X::NV, PLANE = X::PLANE;
     const int r = tid / TPR, c = (tid % TPR) * FPT;
     float amax = 0.0f;
     uint32_t ph[FPT / 2], pm[FPT / 2], pl[FPT / 2];
@@ -499,13 +501,14 @@ __device__ __forceinline__ float xstore_a(__bf16 *As, int tid, const float4 (&a)
 // nullptr), else y (+ residual), rows holding a |x| > kWideLimit recomputed
 // in FP64.  D layout of 16x16x32: lane holds rows 4*(lane/16)+r, column
 // lane%16.
-template <int TM, int TN>
+// TN feature tiles per wave, XBN features and NT threads per workgroup.
+template <int TM, int TN, int XBN = 64 * TN, int NT = 256>
 __device__ __forceinline__ void x3_finish(const GemmArgs &G, float *__restrict__ partial, int32_t *__restrict__ wflags,
                                           const floatx4 (&acc)[TM][TN], const float amax, int *row_wide,
                                           const int64_t n0, const int64_t m0, const int tid) {
-    constexpr int BM = XTile<TM>::BM, XBN = 64 * TN;
+    constexpr int BM = XTile<TM>::BM;
     const int lane = tid & 63, li = lane & 15, q = lane >> 4;
-    if (amax > kWideLimit) row_wide[tid / XTile<TM>::TPR] = 1;
+    if (amax > kWideLimit) row_wide[tid / XTile<TM, NT>::TPR] = 1;
     lds_barrier();
 
     if (partial) {
@@ -781,12 +784,13 @@ __device__ __forceinline__ void unroll_each(F &&f, std::integer_sequence<int, I.
     (f(std::integral_constant<int, I>{}), ...);
 }
 
-template <int TM, int TN, int KU, int DIST, int ODD>
+template <int TM, int TN, int NW, int KU, int DIST, int ODD>
 __device__ __forceinline__ void x3p_slice(const GemmArgs &G, const int64_t n0, const int64_t m0, const int gbeg,
                                           const int gend, const int tid, __bf16 (*As)[3 * XTile<TM>::PLANE],
                                           u32x4v *ws, float *ss, floatx4 (&acc)[TM][TN], float &amax) {
     typedef PairRole<KU, ODD> Role;
-    constexpr int NV = XTile<TM>::NV, PLANE = XTile<TM>::PLANE, FPT = XTile<TM>::FPT, TPR = XTile<TM>::TPR;
+    typedef XTile<TM, 64 * NW> X;
+    constexpr int NV = X::NV, PLANE = X::PLANE, FPT = X::FPT, TPR = X::TPR;
     // Activations run one block further ahead than weights and each
     // block issues them first.  The wave's load counter retires in issue
     // order, so a wait for block k+1's activations then never waits for
@@ -825,12 +829,12 @@ __device__ __forceinline__ void x3p_slice(const GemmArgs &G, const int64_t n0, c
     // a few rows) into ss[row][block] (row stride KS, odd: the 16 rows of
     // an operand read hit distinct banks).  Per-block scale loads of 16
     // rows each would cost as many cache-line requests as the weights.
-    constexpr int XBN = 64 * TN, KS = KU | 1, SE = (XBN * KU + 255) / 256;
+    constexpr int NT = 64 * NW, XBN = 16 * TN * NW, KS = KU | 1, SE = (XBN * KU + NT - 1) / NT;
     const int64_t wrow0 = n0 - (tid >> 6) * 16 * TN;  // the workgroup's first output
     float sreg[SE];
 #pragma unroll
     for (int i = 0; i < SE; ++i) {
-        const int e = tid + 256 * i;
+        const int e = tid + NT * i;
         const int r = e / KU, j = e - r * KU;
         const int64_t row = min(wrow0 + r, G.rows - 1);
         // a block past the slice's end (last slice) is added with a zero scale
@@ -839,7 +843,7 @@ __device__ __forceinline__ void x3p_slice(const GemmArgs &G, const int64_t n0, c
     auto stage_s = [&]() {
 #pragma unroll
         for (int i = 0; i < SE; ++i) {
-            const int e = tid + 256 * i;
+            const int e = tid + NT * i;
             const int r = e / KU, j = e - r * KU;
             if (e < XBN * KU) ss[r * KS + j] = sreg[i];
         }
@@ -891,7 +895,7 @@ __device__ __forceinline__ void x3p_slice(const GemmArgs &G, const int64_t n0, c
     }, std::make_integer_sequence<int, DIST>{});
     stage_s();
     if constexpr (Role::first(0)) stage_w(std::integral_constant<int, 0>{});
-    amax = xstore_a<TM>(As[0], tid, areg[0]);
+    amax = xstore_a<TM, NT>(As[0], tid, areg[0]);
     lds_barrier();
 
     unroll_each([&](auto K) {
@@ -937,7 +941,7 @@ __device__ __forceinline__ void x3p_slice(const GemmArgs &G, const int64_t n0, c
             // the next pair -> the region (after this block's reads of it),
             // block k+1's activations -> the other stage
             if constexpr (Role::first(k + 1)) stage_w(std::integral_constant<int, k + 1>{});
-            amax = fmaxf(amax, xstore_a<TM>(As[v], tid, areg[(k + 1) % DA]));
+            amax = fmaxf(amax, xstore_a<TM, NT>(As[v], tid, areg[(k + 1) % DA]));
             lds_barrier();
         }
     }, std::make_integer_sequence<int, KU>{});
@@ -946,16 +950,20 @@ __device__ __forceinline__ void x3p_slice(const GemmArgs &G, const int64_t n0, c
 // Q8, 16- or 32-row tiles, cols % 128 == 0, rows * cols < 2^32, slices of exactly KU blocks
 // (the last slice may be shorter).  DIST: blocks between a block's loads
 // and its use.
-// Four feature tiles per wave need more than the 256 registers of two
-// workgroups per CU; their grids (outputs above 8192) hold about one
-// workgroup per CU anyway.
-template <int TM, int TN, int KU, int DIST>
-__global__ __launch_bounds__(256, TN == 4 ? 1 : 2) void gemm_x3p_kernel(const GemmArgs G, float *__restrict__ partial,
-                                                          int32_t *__restrict__ wflags, const int kper) {
-    constexpr int BM = XTile<TM>::BM, PLANE = XTile<TM>::PLANE, XBN = 64 * TN;
+// Q8, 16- or 32-row tiles, cols % 128 == 0, rows * cols < 2^32, slices of
+// exactly KU blocks (the last slice may be shorter).  NW waves of TN
+// feature tiles each; DIST: blocks between a block's loads and its use.
+// Eight waves keep two per SIMD in the one workgroup a CU holds, so that
+// one wave's MFMAs overlap another's conversions and LDS waits, while the
+// activation stage stays shared by all the workgroup's features.  Up to
+// eight tiles per workgroup, two workgroups fit a CU.
+template <int TM, int TN, int NW, int KU, int DIST>
+__global__ __launch_bounds__(64 * NW, TN * NW <= 8 ? 2 : 1) void gemm_x3p_kernel(
+    const GemmArgs G, float *__restrict__ partial, int32_t *__restrict__ wflags, const int kper) {
+    constexpr int BM = XTile<TM>::BM, PLANE = XTile<TM>::PLANE, XBN = 16 * TN * NW;
     __shared__ __attribute__((aligned(16))) __bf16 As[2][3 * PLANE];
-    __shared__ u32x4v Ws[4][TN * 128];
-    __shared__ float Ss[64 * TN * (KU | 1)];
+    __shared__ u32x4v Ws[NW][TN * 128];
+    __shared__ float Ss[XBN * (KU | 1)];
     __shared__ int row_wide[BM];
     const int tid = threadIdx.x, wave = tid >> 6;
     const int64_t n0 = (int64_t)blockIdx.x * XBN + wave * 16 * TN, m0 = (int64_t)blockIdx.y * BM;
@@ -970,10 +978,10 @@ __global__ __launch_bounds__(256, TN == 4 ? 1 : 2) void gemm_x3p_kernel(const Ge
         for (int j = 0; j < TN; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
     float amax = 0.0f;
     if (gbeg & 1)
-        x3p_slice<TM, TN, KU, DIST, 1>(G, n0, m0, gbeg, gend, tid, As, Ws[wave], Ss, acc, amax);
+        x3p_slice<TM, TN, NW, KU, DIST, 1>(G, n0, m0, gbeg, gend, tid, As, Ws[wave], Ss, acc, amax);
     else
-        x3p_slice<TM, TN, KU, DIST, 0>(G, n0, m0, gbeg, gend, tid, As, Ws[wave], Ss, acc, amax);
-    x3_finish<TM, TN>(G, partial, wflags, acc, amax, row_wide, n0, m0, tid);
+        x3p_slice<TM, TN, NW, KU, DIST, 0>(G, n0, m0, gbeg, gend, tid, As, Ws[wave], Ss, acc, amax);
+    x3_finish<TM, TN, XBN, 64 * NW>(G, partial, wflags, acc, amax, row_wide, n0, m0, tid);
 }
 
 // The same for four consecutive outputs (rows, y_stride and the plane are
@@ -1198,13 +1206,13 @@ void launch_unrolled(hipStream_t s, dim3 grid, const GemmArgs &a, float *partial
 template <int TN>
 constexpr int kPairDist = 4;
 
-template <int TM, int TN, int KU = 4>
+template <int TM, int TN, int NW, int KU = 4>
 void launch_pairs(hipStream_t s, dim3 grid, const GemmArgs &a, float *partial, int32_t *wflags, int kper) {
     if constexpr (KU <= 12) {
         if (kper == KU)
-            gemm_x3p_kernel<TM, TN, KU, kPairDist<TN>><<<grid, 256, 0, s>>>(a, partial, wflags, kper);
+            gemm_x3p_kernel<TM, TN, NW, KU, kPairDist<TN>><<<grid, 64 * NW, 0, s>>>(a, partial, wflags, kper);
         else
-            launch_pairs<TM, TN, KU + 1>(s, grid, a, partial, wflags, kper);
+            launch_pairs<TM, TN, NW, KU + 1>(s, grid, a, partial, wflags, kper);
     }
 }
 
@@ -1223,12 +1231,19 @@ void launch_tiles(hipStream_t s, const GemmArgs &a, const GemmPlan &p, float *pa
             if constexpr (BMT <= 32) {
                 if (FMT == SRQ_Q8 && p.kper >= 4 && p.kper <= 12 && a.cols % (2 * kBlock) == 0 &&
                     (uint64_t)a.rows * (uint64_t)a.cols <= UINT32_MAX) {
-                    if (p.tn == 1)
-                        launch_pairs<BMT / 16, 1>(s, grid, a, partial, wflags, p.kper);
-                    else if (p.tn == 2)
-                        launch_pairs<BMT / 16, 2>(s, grid, a, partial, wflags, p.kper);
-                    else if constexpr (BMT == 32)  // 16-row plans take at most 2 tiles
-                        launch_pairs<2, 4>(s, grid, a, partial, wflags, p.kper);
+                    // the plan's feature tile (64 * tn); 256 features over 8 waves
+                    // (gate/up 16384x3072 at 17-32 rows: 24.5 -> 22.6 us; 128
+                    // features over 8 waves were slower)
+                    if constexpr (BMT == 32) {
+                        if (p.tn == 2)
+                            launch_pairs<2, 2, 4>(s, grid, a, partial, wflags, p.kper);
+                        else
+                            launch_pairs<2, 2, 8>(s, grid, a, partial, wflags, p.kper);
+                    } else if (p.tn == 1) {
+                        launch_pairs<1, 1, 4>(s, grid, a, partial, wflags, p.kper);
+                    } else {
+                        launch_pairs<1, 2, 4>(s, grid, a, partial, wflags, p.kper);  // 16-row plans: tn <= 2
+                    }
                     return;
                 }
             }
