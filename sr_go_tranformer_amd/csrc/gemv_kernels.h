@@ -1166,6 +1166,12 @@ int launch_t(hipStream_t s, const GemvArgs &a) {
         if ((units / (blocks * kStreamWaves) + 1) * nch >= (1LL << 31))
             return fail(SRQ_EINVAL, "gemv: %lld x %lld exceeds the per-wave step limit", (long long)a.rows,
                         (long long)a.cols);
+        // Q4, one batch row: two units per step, so that their rows share
+        // each read of the activations from LDS (Q4 reads 32 of them per 16
+        // weight bytes).
+        if constexpr (NB == 1 && FMT != SRQ_F32) {
+            if (units >= 2 * blocks * kStreamWaves) return launch_grid<FMT, NB, EPI, NORM, false, 2>(s, a, nch, blocks);
+        }
         // Residuals staged when every wave has at most kResidUnits units and
         // their LDS slice fits.
         if constexpr (EPI == EPI_RESID) {
