@@ -1170,6 +1170,13 @@ int launch_t(hipStream_t s, const GemvArgs &a) {
         // each read of the activations from LDS (Q4 reads 32 of them per 16
         // weight bytes).
         if constexpr (NB == 1 && FMT != SRQ_F32) {
+            // four, for one-row Q4 units, where every wave gets two groups
+            // (28672x4096: 50% -> 53% of peak; 14336x4096, 7 units a wave,
+            // falls from 40.5% to 37%)
+            if constexpr (FMT == SRQ_Q4 && unit_rows_of<EPI>() == 1) {
+                if (units >= 8 * blocks * kStreamWaves)
+                    return launch_grid<FMT, NB, EPI, NORM, false, 4>(s, a, nch, blocks);
+            }
             if (units >= 2 * blocks * kStreamWaves) return launch_grid<FMT, NB, EPI, NORM, false, 2>(s, a, nch, blocks);
         }
         // Residuals staged when every wave has at most kResidUnits units and
