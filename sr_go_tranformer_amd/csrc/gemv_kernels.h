@@ -1166,10 +1166,11 @@ int launch_t(hipStream_t s, const GemvArgs &a) {
         if ((units / (blocks * kStreamWaves) + 1) * nch >= (1LL << 31))
             return fail(SRQ_EINVAL, "gemv: %lld x %lld exceeds the per-wave step limit", (long long)a.rows,
                         (long long)a.cols);
-        // Q4, one batch row: two units per step, so that their rows share
-        // each read of the activations from LDS (Q4 reads 32 of them per 16
-        // weight bytes).
-        if constexpr (NB == 1 && FMT != SRQ_F32) {
+        // One batch row: two units per step, so that their rows share each
+        // read of the activations from LDS (Q4 reads 32 of them per 16
+        // weight bytes).  Q8 pairs only one-row units: its two-row SwiGLU
+        // units in groups of two ran slower (gate/up 22.5 -> 23.1 us).
+        if constexpr (NB == 1 && (FMT == SRQ_Q4 || (FMT == SRQ_Q8 && unit_rows_of<EPI>() == 1))) {
             // four, for one-row Q4 units, where every wave gets two groups
             // (28672x4096: 50% -> 53% of peak; 14336x4096, 7 units a wave,
             // falls from 40.5% to 37%)
