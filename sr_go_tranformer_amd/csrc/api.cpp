@@ -298,6 +298,7 @@ RowMeta make_meta(srq_exec *e, srq_model *m, int layer, int32_t pt_stride, const
     r.layer = layer;
     r.kvoff = nullptr;
     r.rope_cs = nullptr;
+    r.one_sess = 0;
     (void)m;
     return r;
 }
@@ -1077,6 +1078,7 @@ struct StepMeta {
     int32_t *tiles = nullptr;  // query tiles {first row, rows} (AttnArgs::tiles)
     int32_t ntiles = 0;
     bool plan_ready = false;   // the row plan in ws.PLAN is already current (decoder)
+    bool one_sess = false;     // every row belongs to session 0 (RowMeta::one_sess)
 };
 
 // Layout of the packed metadata buffer (device and pinned host mirror): at
@@ -1178,6 +1180,7 @@ int enqueue_layers(srq_exec *e, Workspace &ws, srq_model *m, srq_pool *pool, int
         RowMeta meta = make_meta(e, m, l, dm.pt_stride, dm.pos, dm.sess, dm.pages, pool);
         meta.kvoff = kvoff;
         meta.rope_cs = rope_cs;
+        meta.one_sess = dm.one_sess ? 1 : 0;
         if (!use_gemm) {
             for (int32_t r0 = 0; r0 < n; r0 += nbq) {
                 GemvArgs a{};
@@ -1376,6 +1379,7 @@ extern "C" int srq_step(srq_exec *e, srq_model *m, int32_t sessions, srq_cache *
     }
     SRQ_HIP(hipMemcpyAsync(ws.meta.p, e->h_meta, words * 4, hipMemcpyHostToDevice, e->stream));
     StepMeta dm = carve(as<int32_t>(ws.meta), n, sessions, pt_stride);
+    dm.one_sess = sessions == 1;
     dm.ntiles = ntiles;
 
     // Embedding rows (copyRow, M:6364-6375).
@@ -1521,6 +1525,7 @@ static int enqueue_decode_step(srq_decoder *d) {
     dm.pages = pt;
     dm.pt_stride = d->pt_stride;
     dm.plan_ready = true;
+    dm.one_sess = true;  // the decoder's one session is session 0
     Workspace &ws = d->ws;
     SRQ_CHECK(enqueue_layers(e, ws, m, d->c->p, 1, d->start_pos + d->max_steps, dm, nullptr));
     SRQ_CHECK(enqueue_head(e, ws, m, as<float>(ws.X), 1));

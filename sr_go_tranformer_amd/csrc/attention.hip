@@ -64,7 +64,7 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const AttnArgs A, float
     const int row = blockIdx.x, kh = blockIdx.y, sp = blockIdx.z;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int hd = A.head_dim, kvdim = A.kv_heads * hd, G = A.heads / A.kv_heads;
-    const int pos = A.meta.pos[row], sess = A.meta.sess[row];
+    const int pos = A.meta.pos[row], sess = A.meta.one_sess ? 0 : A.meta.sess[row];
     const int len = pos + 1, s0 = sp * kSplit, s1 = min(len, s0 + kSplit), ns = s1 - s0;
     if (ns <= 0) {
         // Empty split: contributes nothing to the combine.
@@ -278,7 +278,7 @@ __device__ __forceinline__ bool split_partial(const AttnArgs &A, float *part, in
         const int i = tid + 256 * r, g = i / HD, j = i - g * HD;
         qv[r] = i < G * HD ? A.q[(int64_t)row * A.heads * HD + (int64_t)(kh * G + g) * HD + j] : 0.0f;
     }
-    const int pos = A.meta.pos[row], sess = A.meta.sess[row];
+    const int pos = A.meta.pos[row], sess = A.meta.one_sess ? 0 : A.meta.sess[row];
     const int s0 = sp * kSplit, pi = s0 / kPageTokens;
     const int32_t *ptrow = A.meta.pages + (int64_t)sess * A.meta.pt_stride;
     const int pg0 = ptrow[min(pi, A.meta.pt_stride - 1)], pg1 = ptrow[min(pi + 1, A.meta.pt_stride - 1)];

@@ -76,6 +76,9 @@ struct RowMeta {
     // Row plan (launch_row_plan), used by the fused GEMV epilogue:
     const int64_t *kvoff;      // [n] element offset of the row's K row in layer 0
     const float *rope_cs;      // [n x head_dim] {cos, sin} of the row's position, interleaved
+    // Every row belongs to session 0 (one-session steps, the decoder): a
+    // row's page-table entries need no load of its session first.
+    int32_t one_sess;
 };
 
 struct GemvArgs {
