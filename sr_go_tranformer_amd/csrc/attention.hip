@@ -228,43 +228,74 @@ __device__ __forceinline__ double wave_sum(double v) {
     return v;
 }
 
+// Butterfly steps over lane distances K, 2K, ..., up to KMAX.
+template <int K, int KMAX>
+__device__ __forceinline__ float xor_max_from(float v) {
+    if constexpr (K <= KMAX) return xor_max_from<2 * K, KMAX>(xor_max<K>(v));
+    return v;
+}
+template <int K, int KMAX>
+__device__ __forceinline__ double xor_add_from(double v) {
+    if constexpr (K <= KMAX) return xor_add_from<2 * K, KMAX>(xor_add<K>(v));
+    return v;
+}
+template <int K, int KMAX>
+__device__ __forceinline__ float xor_fadd_from(float v) {
+    if constexpr (K <= KMAX) {
+        int a, b;
+        xor_pair<K>(__float_as_int(v), a, b);
+        return xor_fadd_from<2 * K, KMAX>(__int_as_float(a) + __int_as_float(b));
+    }
+    return v;
+}
+
 // LDS of split_partial: the GQA group's queries, each wave's softmax
-// weights and each wave's partial over its 16 keys.
-constexpr int kWaveKeys = kSplit / 4;  // keys per wave
+// weights and each wave's partial over its keys.
+constexpr int kSplitWaves = 8;                   // waves per split workgroup
+constexpr int kSplitThreads = 64 * kSplitWaves;
+constexpr int kWaveKeys = kSplit / kSplitWaves;  // keys per wave
+constexpr int kKeyLanes = 64 / kWaveKeys;        // lanes per key while scoring
+static_assert(kWaveKeys % 4 == 0 && kKeyLanes >= 4, "split layout");
 template <int HD>
 struct SplitStage {
     alignas(16) float qs[kMaxGroup * HD];
-    alignas(16) float ps[4][kMaxGroup][kWaveKeys];  // [wave][head][key]
-    float wm[4][kMaxGroup];             // wave partials: max,
-    double wl[4][kMaxGroup];            //   FP64 sum,
-    float wo[4][kMaxGroup][HD];         //   weighted V sum
+    alignas(16) float ps[kSplitWaves][kMaxGroup][kWaveKeys];  // [wave][head][key]
+    float wm[kSplitWaves][kMaxGroup];                         // wave partials: max,
+    double wl[kSplitWaves][kMaxGroup];                        //   FP64 sum,
+    float wo[kSplitWaves][kMaxGroup][HD];                     //   weighted V sum
 };
 
 // Partial {m, l, o} of split sp of (row, kv head kh) for every query head of
-// the group, head_dim 64 / 128, 256 threads.  All K and V rows of the split
-// are loaded into registers at once (one round of memory latency).  Wave w
-// takes keys 16w .. 16w+15 of the split for every head of the group:
-//   scores: lane 4k + t holds dims [t*HD/4, +HD/4) of key k; per head a
-//     dot over those dims (FMA in dim order), then the four quarters added
-//     as ((q0 + q1) + (q2 + q3)) by a butterfly, * f32(1/sqrt(hd)); lane
-//     4k + t keeps heads t, t+4
+// the group, head_dim 64 / 128, kSplitThreads threads.  All K and V rows of
+// the split are loaded into registers at once (one round of memory
+// latency).  Wave w takes keys 8w .. 8w+7 of the split for every head of the
+// group:
+//   scores: lane 8k + t holds the float4s t, t+8, t+16, ... of key k (so
+//     one load instruction reads whole 128-byte lines of eight keys); per
+//     head a dot over those dims (FMA in dim order), then the eight parts
+//     added by a butterfly over distances 1, 2, 4, * f32(1/sqrt(hd)); lane
+//     8k + t keeps head t (of four per pass)
 //   wave softmax per head: m_w = max over its keys, e = exp((double)s - m_w),
 //     l_w = FP64 butterfly sum, p = f32(e)
 //   o_w[j] = sum over its keys of p_k v_k[j], FMA in key order; lane holds
 //     dims HD/64 * lane + ...
-// then wave w merges head w (and w+4) over the four waves, in wave order:
+// then wave w merges head w over the eight waves, in wave order:
 //   m = max m_w, c_w = exp((double)m_w - m), l = sum l_w c_w (FP64,
-//   butterfly over the four), o[j] = sum f32(c_w) o_w[j] (FMA).
-// Keys past the row's positions weigh nothing.  COHERENT: stored with
-// agent-scope stores (publish) for the fused merge.  Returns false, writing
-// nothing, for a split past the row's positions.
+//   butterfly over the eight), o[j] = sum f32(c_w) o_w[j] (FMA).
+// Eight waves of eight keys rather than four of sixteen: each wave's
+// dependent chain of scoring, softmax and P.V is half as long, and two
+// waves share each SIMD.  Keys past the row's positions weigh nothing.
+// COHERENT: stored with agent-scope stores (publish) for the fused merge,
+// except that a row of one split stores its merged output itself.
+// Returns false, writing nothing, for a split past the row's positions.
 template <int HD, bool COHERENT>
 __device__ __forceinline__ bool split_partial(const AttnArgs &A, float *part, int nsplit, int row, int kh, int sp,
                                               SplitStage<HD> &S) {
-    constexpr int QD = HD / 4;    // dims of a key per scoring lane
-    constexpr int DPL = HD / 64;  // V dims per lane
+    constexpr int QV = HD / (4 * kKeyLanes);  // float4s of a key per scoring lane
+    constexpr int DPL = HD / 64;              // V dims per lane
     typedef typename std::conditional<DPL == 2, float2, float>::type VDims;
-    constexpr int QPT = kMaxGroup * HD / 256;  // query values per thread, at most
+    constexpr int QPT = (kMaxGroup * HD + kSplitThreads - 1) / kSplitThreads;  // query values per thread, at most
+    static_assert(QV >= 1, "head_dim");
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int kvdim = A.kv_heads * HD, G = A.heads / A.kv_heads;
     // The loads form a chain (row meta -> page table -> K/V): the queries,
@@ -275,7 +306,7 @@ __device__ __forceinline__ bool split_partial(const AttnArgs &A, float *part, in
     float qv[QPT];
 #pragma unroll
     for (int r = 0; r < QPT; ++r) {
-        const int i = tid + 256 * r, g = i / HD, j = i - g * HD;
+        const int i = tid + kSplitThreads * r, g = i / HD, j = i - g * HD;
         qv[r] = i < G * HD ? A.q[(int64_t)row * A.heads * HD + (int64_t)(kh * G + g) * HD + j] : 0.0f;
     }
     const int pos = A.meta.pos[row], sess = A.meta.one_sess ? 0 : A.meta.sess[row];
@@ -295,27 +326,27 @@ __device__ __forceinline__ bool split_partial(const AttnArgs &A, float *part, in
         const float *pb = s < kPageTokens ? pb0 : pb1;
         return pb + (int64_t)which * kPageTokens * kvdim + (int64_t)(s & (kPageTokens - 1)) * kvdim;
     };
-    const int kq = lane >> 2, qt = lane & 3;  // scoring: key kq of the wave, quarter qt
+    const int kq = lane / kKeyLanes, qt = lane % kKeyLanes;  // scoring: key kq of the wave, part qt
     const int key0 = kWaveKeys * wave;
-    float4 kr[QD / 4];
+    float4 kr[QV];
     {
-        const float4 *k = (const float4 *)(key_row(key0 + kq, 0) + qt * QD);
+        const float4 *k = (const float4 *)key_row(key0 + kq, 0) + qt;
 #pragma unroll
-        for (int u = 0; u < QD / 4; ++u) kr[u] = k[u];
+        for (int u = 0; u < QV; ++u) kr[u] = k[u * kKeyLanes];
     }
     VDims vr[kWaveKeys];
 #pragma unroll
     for (int k = 0; k < kWaveKeys; ++k) vr[k] = ((const VDims *)key_row(key0 + k, 1))[lane];
 #pragma unroll
     for (int r = 0; r < QPT; ++r)
-        if (tid + 256 * r < G * HD) S.qs[tid + 256 * r] = qv[r];
+        if (tid + kSplitThreads * r < G * HD) S.qs[tid + kSplitThreads * r] = qv[r];
     __syncthreads();
 
     const float scale = (float)(1.0 / sqrt((double)HD));
     const bool kvalid = key0 + kq < ns;
     for (int h0 = 0; h0 < G; h0 += 4) {
         const int nh = min(4, G - h0);
-        // scores of this lane's key quarter for heads h0 .. h0+3 (slots past
+        // scores of this lane's key part for heads h0 .. h0+3 (slots past
         // the group repeat its last head, unused)
         int hs[4];
 #pragma unroll
@@ -324,10 +355,10 @@ __device__ __forceinline__ bool split_partial(const AttnArgs &A, float *part, in
 #pragma unroll
         for (int g = 0; g < 4; ++g) d[g] = 0.0f;
 #pragma unroll
-        for (int u = 0; u < QD / 4; ++u) {
+        for (int u = 0; u < QV; ++u) {
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
-                const float4 q = ((const float4 *)(S.qs + hs[g] * HD + qt * QD))[u];
+                const float4 q = ((const float4 *)(S.qs + hs[g] * HD))[u * kKeyLanes + qt];
                 d[g] = __builtin_fmaf(q.x, kr[u].x, d[g]);
                 d[g] = __builtin_fmaf(q.y, kr[u].y, d[g]);
                 d[g] = __builtin_fmaf(q.z, kr[u].z, d[g]);
@@ -335,21 +366,14 @@ __device__ __forceinline__ bool split_partial(const AttnArgs &A, float *part, in
             }
         }
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-            int a, b;
-            xor_pair<1>(__float_as_int(d[g]), a, b);
-            d[g] = __int_as_float(a) + __int_as_float(b);
-            xor_pair<2>(__float_as_int(d[g]), a, b);
-            d[g] = __int_as_float(a) + __int_as_float(b);
-        }
-        // lane 4k + p: head h0 + p
+        for (int g = 0; g < 4; ++g) d[g] = xor_fadd_from<1, kKeyLanes / 2>(d[g]);
+        // lane kKeyLanes*k + p: head h0 + p
         const float sc = (qt == 0 ? d[0] : qt == 1 ? d[1] : qt == 2 ? d[2] : d[3]) * scale;
         const bool valid = kvalid && qt < nh;
         float m = valid ? sc : -FLT_MAX;
-        m = xor_max<4>(m), m = xor_max<8>(m), m = xor_max<16>(m), m = xor_max<32>(m);
+        m = xor_max_from<kKeyLanes, 32>(m);
         double e = valid ? exp((double)sc - (double)m) : 0.0;
-        double l = e;
-        l = xor_add<4>(l), l = xor_add<8>(l), l = xor_add<16>(l), l = xor_add<32>(l);
+        const double l = xor_add_from<kKeyLanes, 32>(e);
         if (qt < nh) {
             S.ps[wave][h0 + qt][kq] = (float)e;
             if (kq == 0) {
@@ -395,23 +419,34 @@ __device__ __forceinline__ bool split_partial(const AttnArgs &A, float *part, in
     }
     __syncthreads();
 
-    // wave w merges head w (and w + 4) over the four waves
-    for (int h = wave; h < G; h += 4) {
-        const int src = lane & 3;
+    // wave w merges head w over the eight waves
+    for (int h = wave; h < G; h += kSplitWaves) {
+        const int src = lane & (kSplitWaves - 1);
         const float mw = S.wm[src][h];
         const double lw = S.wl[src][h];
-        const float M = xor_max<2>(xor_max<1>(mw));
+        const float M = xor_max_from<1, kSplitWaves / 2>(mw);
         const double c = exp((double)mw - (double)M);
-        const double l = xor_add<2>(xor_add<1>(lw * c));
+        const double l = xor_add_from<1, kSplitWaves / 2>(lw * c);
         const float cf = (float)c;
         float o[DPL];
 #pragma unroll
         for (int t = 0; t < DPL; ++t) o[t] = 0.0f;
 #pragma unroll
-        for (int w = 0; w < 4; ++w) {
+        for (int w = 0; w < kSplitWaves; ++w) {
             const float cw = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(cf), w));
 #pragma unroll
             for (int t = 0; t < DPL; ++t) o[t] = __builtin_fmaf(cw, S.wo[w][h][DPL * lane + t], o[t]);
+        }
+        if (COHERENT && len <= kSplit) {
+            // The row's only split: merge_wave's arithmetic on one partial
+            // (M and l pass through unchanged, the factor f32(exp(m - lse)),
+            // one FMA from zero), stored as the output with no exchange.
+            const double lse = (double)M + log(l);
+            const float cf1 = (float)exp((double)M - lse);
+            float *out = A.out + (int64_t)row * A.heads * HD + (int64_t)(kh * G + h) * HD + DPL * lane;
+#pragma unroll
+            for (int t = 0; t < DPL; ++t) out[t] = __builtin_fmaf(cf1, o[t], 0.0f);
+            continue;
         }
         float *p = partial(part, row, kh * G + h, sp, A.heads, nsplit, HD);
         if constexpr (COHERENT) {
@@ -439,13 +474,13 @@ __device__ __forceinline__ bool split_partial(const AttnArgs &A, float *part, in
 // Split kernel for head_dim 64 / 128 (split_partial); the combine kernel
 // merges.  Splits past a row's positions write the empty partial.
 template <int HD>
-__global__ __launch_bounds__(256) void attn_split_fast_kernel(const AttnArgs A, float *__restrict__ part,
-                                                              int nsplit) {
+__global__ __launch_bounds__(kSplitThreads) void attn_split_fast_kernel(const AttnArgs A, float *__restrict__ part,
+                                                                        int nsplit) {
     __shared__ SplitStage<HD> S;
     const int row = blockIdx.x, kh = blockIdx.y, sp = blockIdx.z;
     if (split_partial<HD, false>(A, part, nsplit, row, kh, sp, S)) return;
     const int G = A.heads / A.kv_heads;
-    for (int i = threadIdx.x; i < G * (HD + 4); i += 256) {
+    for (int i = threadIdx.x; i < G * (HD + 4); i += kSplitThreads) {
         const int g = i / (HD + 4), k = i - g * (HD + 4);
         float *p = partial(part, row, kh * G + g, sp, A.heads, nsplit, HD);
         p[k] = k == 0 ? -FLT_MAX : 0.0f;
@@ -479,11 +514,15 @@ __device__ __forceinline__ void merge_wave(const AttnArgs &A, const float *part,
     const float *pl = partial((float *)part, row, h, min(lane, used - 1), A.heads, nsplit, HD);
     const float mraw = fetch(pl);
     const double lraw = fetch((const double *)(pl + 2));
-    Dims v[kMergeBatch];
+    // The first kPre splits' dims load with {m, l}; up to kMergeBatch
+    // splits, the rest load after the factors (a second round, only past
+    // kPre splits), so that the fused kernel keeps to 128 registers.
+    constexpr int kPre = kMergeBatch / 2;
+    Dims v[kPre];
     const bool pre = used <= kMergeBatch;
     if (pre) {
 #pragma unroll
-        for (int b = 0; b < kMergeBatch; ++b)
+        for (int b = 0; b < kPre; ++b)
             if (b < used) v[b] = fetch((const Dims *)(pb + (int64_t)b * (HD + 4)));
     }
     float M = lane < used ? mraw : -FLT_MAX;
@@ -511,8 +550,17 @@ __device__ __forceinline__ void merge_wave(const AttnArgs &A, const float *part,
     if (pre) {
         const float cf = lane < used ? (float)exp((double)mraw - lse) : 0.0f;
 #pragma unroll
-        for (int b = 0; b < kMergeBatch; ++b)
+        for (int b = 0; b < kPre; ++b)
             if (b < used) acc(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(cf), b)), v[b]);
+        if (used > kPre) {
+#pragma unroll
+            for (int b = 0; b < kPre; ++b)
+                if (kPre + b < used) v[b] = fetch((const Dims *)(pb + (int64_t)(kPre + b) * (HD + 4)));
+#pragma unroll
+            for (int b = 0; b < kPre; ++b)
+                if (kPre + b < used)
+                    acc(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(cf), kPre + b)), v[b]);
+        }
     } else {
         // merge_splits' order: past kChainSplits (up to kMergeChunk) splits
         // the dims sum ng groups of `per` consecutive splits, each from
@@ -820,14 +868,15 @@ __device__ __forceinline__ void merge_splits(const AttnArgs &A, const float *par
 // per (row, kv head), reset by the merging workgroup, so the kernel replays
 // without clearing).
 template <int HD>
-__global__ __launch_bounds__(256) void attn_fused_kernel(const AttnArgs A, float *__restrict__ part, int nsplit,
-                                                         int32_t *__restrict__ counters) {
+__global__ __launch_bounds__(kSplitThreads, 4) void attn_fused_kernel(const AttnArgs A, float *__restrict__ part,
+                                                                   int nsplit, int32_t *__restrict__ counters) {
     __shared__ SplitStage<HD> S;
     __shared__ int last;
     const int bid = blockIdx.x, row = bid % A.n, kh = (bid / A.n) % A.kv_heads, sp = bid / (A.n * A.kv_heads);
     const int tid = threadIdx.x, wave = tid >> 6;
     if (!split_partial<HD, true>(A, part, nsplit, row, kh, sp, S)) return;  // no partial, no count
     const int G = A.heads / A.kv_heads, used = (A.meta.pos[row] + kSplit) / kSplit;
+    if (used == 1) return;  // a row's only split wrote its output
     // Each wave's partial stores complete before the barrier, so the split
     // is counted only once all of them are visible device-wide.
     //
@@ -852,7 +901,7 @@ __global__ __launch_bounds__(256) void attn_fused_kernel(const AttnArgs A, float
     if (!last) return;
     if (tid == 0) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     // one wave per head merges on its own
-    for (int g = wave; g < G; g += 4) merge_wave<HD>(A, part, nsplit, row, kh * G + g, used);
+    for (int g = wave; g < G; g += kSplitWaves) merge_wave<HD>(A, part, nsplit, row, kh * G + g, used);
 }
 
 // lse and the weighted sum of split partials for one (row, head); split i
@@ -1109,16 +1158,16 @@ int launch_attention(hipStream_t s, const AttnArgs &a, float *scratch, int32_t *
         // merges.
         const dim3 g1((unsigned)((int64_t)a.n * a.kv_heads * nsplit));
         if (a.head_dim == 128)
-            attn_fused_kernel<128><<<g1, 256, 0, s>>>(a, scratch, nsplit, counters);
+            attn_fused_kernel<128><<<g1, kSplitThreads, 0, s>>>(a, scratch, nsplit, counters);
         else
-            attn_fused_kernel<64><<<g1, 256, 0, s>>>(a, scratch, nsplit, counters);
+            attn_fused_kernel<64><<<g1, kSplitThreads, 0, s>>>(a, scratch, nsplit, counters);
         SRQ_HIP(hipGetLastError());
         return SRQ_OK;
     }
     if (a.head_dim == 128)
-        attn_split_fast_kernel<128><<<grid, 256, 0, s>>>(a, scratch, nsplit);
+        attn_split_fast_kernel<128><<<grid, kSplitThreads, 0, s>>>(a, scratch, nsplit);
     else if (a.head_dim == 64)
-        attn_split_fast_kernel<64><<<grid, 256, 0, s>>>(a, scratch, nsplit);
+        attn_split_fast_kernel<64><<<grid, kSplitThreads, 0, s>>>(a, scratch, nsplit);
     else
         attn_split_kernel<<<grid, 256, 0, s>>>(a, scratch, nsplit);
     SRQ_HIP(hipGetLastError());
