@@ -19,9 +19,10 @@
 //  - LDS holds x permuted so that the 16 B a lane reads for its columns are
 //    consecutive across lanes (conflict-free ds_read_b128).
 //  - Q8 codes convert with one SDWA sign-extending v_cvt_f32_i32 each, then
-//    one FMA per weight and batch row.  Q4 nibbles are shifted into the high
-//    half of each byte, which sign-extends to 16*code exactly; the factor 16
-//    is removed exactly after the block partial.
+//    one FMA per weight and batch row.  Q4 nibbles convert with one SDWA
+//    v_cvt_off_f32_i4 each (the low nibble of a selected byte, as code/16
+//    exactly; the odd columns from the word shifted right by 4); the factor
+//    1/16 is removed exactly after the block partial.
 //  - Per lane: partial over its 16/32 weights of one 64-column block, then
 //    acc = fma(partial, scale, acc); lanes are combined by a fixed xor tree.
 //    The arithmetic of a (row, output) pair never depends on n or on the
@@ -81,8 +82,24 @@ __device__ __forceinline__ double wave_sum_d(double v) {
 
 __device__ __forceinline__ float sext8(uint32_t w, int byte) { return (float)(int32_t)(int8_t)(w >> (8 * byte)); }
 
+// code/16 of the signed nibble in bits [3:0] of byte B of w: one
+// v_cvt_off_f32_i4 with an SDWA byte select (exact; 8 -> -0.5, 7 -> 0.4375).
+template <int B>
+__device__ __forceinline__ float nib16(uint32_t w) {
+    float r;
+    if constexpr (B == 0)
+        asm("v_cvt_off_f32_i4_sdwa %0, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_0" : "=v"(r) : "v"(w));
+    else if constexpr (B == 1)
+        asm("v_cvt_off_f32_i4_sdwa %0, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_1" : "=v"(r) : "v"(w));
+    else if constexpr (B == 2)
+        asm("v_cvt_off_f32_i4_sdwa %0, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_2" : "=v"(r) : "v"(w));
+    else
+        asm("v_cvt_off_f32_i4_sdwa %0, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_3" : "=v"(r) : "v"(w));
+    return r;
+}
+
 // Decode one lane's weights of one chunk for the FAST layouts.  Q4 yields
-// 16*code (see header comment).
+// code/16 (see header comment).
 template <int FMT>
 __device__ __forceinline__ void decode16(const uint4 raw, float *w) {
     const uint32_t d[4] = {raw.x, raw.y, raw.z, raw.w};
@@ -97,17 +114,11 @@ __device__ __forceinline__ void decode16(const uint4 raw, float *w) {
     } else if constexpr (FMT == SRQ_Q4) {
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-            uint32_t lo = (d[k] << 4) & 0xF0F0F0F0u;  // even columns, *16
-            uint32_t hi = d[k] & 0xF0F0F0F0u;         // odd columns, *16
-            // Keep the two masked words whole: otherwise the compiler folds
-            // the mask into every byte (sign-extend, mask, convert) instead
-            // of one SDWA sign-extending convert per weight (Q4 GEMV +13%).
-            asm volatile("" : "+v"(lo), "+v"(hi));
-#pragma unroll
-            for (int b = 0; b < 4; ++b) {
-                w[8 * k + 2 * b] = sext8(lo, b);
-                w[8 * k + 2 * b + 1] = sext8(hi, b);
-            }
+            const uint32_t hi = d[k] >> 4;  // odd columns in the low nibbles
+            w[8 * k + 0] = nib16<0>(d[k]), w[8 * k + 1] = nib16<0>(hi);
+            w[8 * k + 2] = nib16<1>(d[k]), w[8 * k + 3] = nib16<1>(hi);
+            w[8 * k + 4] = nib16<2>(d[k]), w[8 * k + 5] = nib16<2>(hi);
+            w[8 * k + 6] = nib16<3>(d[k]), w[8 * k + 7] = nib16<3>(hi);
         }
     } else {
         w[0] = __uint_as_float(raw.x);
@@ -310,8 +321,8 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const GemvArgs A) {
                             p1 = __builtin_fmaf(xv.w, wv1[4 * q + 3], p1);
                         }
                         if constexpr (FMT == SRQ_Q4) {
-                            p0 *= 0.0625f;  // exact: undo the *16 of the nibble decode
-                            p1 *= 0.0625f;
+                            p0 *= 16.0f;  // exact: undo the /16 of the nibble decode
+                            p1 *= 16.0f;
                         }
                         if constexpr (FMT == SRQ_F32) {
                             acc0[b] += p0;
@@ -1017,7 +1028,7 @@ __global__ __launch_bounds__(kStreamThreads) void gemv_stream_kernel(const GemvA
                         float p = 0.0f;
 #pragma unroll
                         for (int e = 0; e < E; ++e) p = __builtin_fmaf(xv[e], wv[i][e], p);
-                        if constexpr (FMT == SRQ_Q4) p *= 0.0625f;  // exact: undo the *16 decode
+                        if constexpr (FMT == SRQ_Q4) p *= 16.0f;  // exact: undo the /16 decode
                         acc[i][b] = __builtin_fmaf(p, scale[i], acc[i][b]);
                     }
                 }
