@@ -422,18 +422,17 @@ __device__ __forceinline__ void xcodes(const typename XRaw<FMT>::type raw, bf16x
             }
         }
     } else {
+        // code/16 (exact in bf16), one SDWA convert per nibble; the block's
+        // scale carries the factor 16 back (SRQ_CONVERT), so the product
+        // block * scale is unchanged bit for bit
 #pragma unroll
         for (int w = 0; w < 2; ++w) {
-            const uint32_t d = raw[w];
-#pragma unroll
-            for (int b = 0; b < 4; ++b) {
-                const float lo = (float)(((int32_t)(d << (28 - 8 * b))) >> 28);
-                const float hi = (float)(((int32_t)(d << (24 - 8 * b))) >> 28);
-                if (w == 0)
-                    p0[b] = pk_hi16(lo, hi);
-                else
-                    p1[b] = pk_hi16(lo, hi);
-            }
+            const uint32_t d = raw[w], h = d >> 4;
+            u32x4v &p = w == 0 ? p0 : p1;
+            p[0] = pk_hi16(nib16<0>(d), nib16<0>(h));
+            p[1] = pk_hi16(nib16<1>(d), nib16<1>(h));
+            p[2] = pk_hi16(nib16<2>(d), nib16<2>(h));
+            p[3] = pk_hi16(nib16<3>(d), nib16<3>(h));
         }
     }
     h0 = __builtin_bit_cast(bf16x8, p0);
@@ -619,7 +618,7 @@ __global__ __launch_bounds__(256, 2) void gemm_x3_kernel(const GemmArgs G, float
 #define SRQ_CONVERT(slot, dst)                                                      \
     _Pragma("unroll") for (int tn = 0; tn < TN; ++tn) {                              \
         xcodes<FMT>(raw[slot][tn], b[dst][tn][0], b[dst][tn][1]);                    \
-        s[dst][tn] = sc[slot][tn];                                                   \
+        s[dst][tn] = FMT == SRQ_Q4 ? 16.0f * sc[slot][tn] : sc[slot][tn];           \
     }
 
     SRQ_LOAD_B(gbeg, 0);

@@ -82,22 +82,6 @@ __device__ __forceinline__ double wave_sum_d(double v) {
 
 __device__ __forceinline__ float sext8(uint32_t w, int byte) { return (float)(int32_t)(int8_t)(w >> (8 * byte)); }
 
-// code/16 of the signed nibble in bits [3:0] of byte B of w: one
-// v_cvt_off_f32_i4 with an SDWA byte select (exact; 8 -> -0.5, 7 -> 0.4375).
-template <int B>
-__device__ __forceinline__ float nib16(uint32_t w) {
-    float r;
-    if constexpr (B == 0)
-        asm("v_cvt_off_f32_i4_sdwa %0, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_0" : "=v"(r) : "v"(w));
-    else if constexpr (B == 1)
-        asm("v_cvt_off_f32_i4_sdwa %0, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_1" : "=v"(r) : "v"(w));
-    else if constexpr (B == 2)
-        asm("v_cvt_off_f32_i4_sdwa %0, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_2" : "=v"(r) : "v"(w));
-    else
-        asm("v_cvt_off_f32_i4_sdwa %0, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_3" : "=v"(r) : "v"(w));
-    return r;
-}
-
 // Decode one lane's weights of one chunk for the FAST layouts.  Q4 yields
 // code/16 (see header comment).
 template <int FMT>

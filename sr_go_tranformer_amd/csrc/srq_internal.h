@@ -29,6 +29,22 @@ __device__ __forceinline__ uint2 ld_stream8(const void *p) {
     return make_uint2(v.x, v.y);
 }
 
+// code/16 of the signed nibble in bits [3:0] of byte B of w: one
+// v_cvt_off_f32_i4 with an SDWA byte select (exact; 8 -> -0.5, 7 -> 0.4375).
+template <int B>
+__device__ __forceinline__ float nib16(uint32_t w) {
+    float r;
+    if constexpr (B == 0)
+        asm("v_cvt_off_f32_i4_sdwa %0, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_0" : "=v"(r) : "v"(w));
+    else if constexpr (B == 1)
+        asm("v_cvt_off_f32_i4_sdwa %0, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_1" : "=v"(r) : "v"(w));
+    else if constexpr (B == 2)
+        asm("v_cvt_off_f32_i4_sdwa %0, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_2" : "=v"(r) : "v"(w));
+    else
+        asm("v_cvt_off_f32_i4_sdwa %0, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_3" : "=v"(r) : "v"(w));
+    return r;
+}
+
 // Error reporting: sets the calling thread's message and returns code.
 int fail(int code, const char *fmt, ...);
 void clear_error();
