@@ -559,6 +559,42 @@ __device__ __forceinline__ void x3_finish(const GemmArgs &G, float *__restrict__
 // in flight.  Rows past the ends are clamped (weights: row rows-1;
 // activations: row n-1) and their outputs are never stored, so the block
 // body has no per-lane branches.
+// MFMAs of one block for a wave's TM x TN tiles.  Each tile accumulates its
+// six products (planes lo, mid, hi; halves 0, 1) from zero in that order,
+// then acc += blk * scale (zero for a block past the slice's end).  The
+// tiles of one row of tiles run interleaved -- product j of every tile
+// before product j + 1 of any -- so that consecutive MFMAs do not depend
+// on each other; each tile's own order, and so every bit, is unchanged.
+template <int TM, int TN>
+__device__ __forceinline__ void x3_block(const __bf16 *as, int li, int q, const bf16x8 (&b)[TN][2],
+                                         const float (&s)[TN], bool live, floatx4 (&acc)[TM][TN]) {
+    constexpr int PLANE = XTile<TM>::PLANE;
+#pragma unroll
+    for (int tm = 0; tm < TM; ++tm) {
+        bf16x8 a[3][2];
+#pragma unroll
+        for (int t = 2; t >= 0; --t)
+#pragma unroll
+            for (int h = 0; h < 2; ++h) a[t][h] = *(const bf16x8 *)(as + t * PLANE + (tm * 16 + li) * XLD + 16 * q + 8 * h);
+        floatx4 blk[TN];
+#pragma unroll
+        for (int tn = 0; tn < TN; ++tn) blk[tn] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int t = 2; t >= 0; --t)
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+                for (int tn = 0; tn < TN; ++tn)
+                    blk[tn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[t][h], b[tn][h], blk[tn], 0, 0, 0);
+#pragma unroll
+        for (int tn = 0; tn < TN; ++tn) {
+            const float sc_u = live ? s[tn] : 0.0f;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[tm][tn][r] = __builtin_fmaf(blk[tn][r], sc_u, acc[tm][tn][r]);
+        }
+    }
+}
+
 template <int FMT, int TM, int TN, int KU>
 __global__ __launch_bounds__(256, 2) void gemm_x3_kernel(const GemmArgs G, float *__restrict__ partial,
                                                                        int32_t *__restrict__ wflags, const int kper) {
@@ -655,28 +691,7 @@ __global__ __launch_bounds__(256, 2) void gemm_x3_kernel(const GemmArgs G, float
                 __builtin_amdgcn_sched_barrier(0);
                 SRQ_LOAD_B(min(g + 3, glast), v);
             }
-            const __bf16 *as = As[u];
-#pragma unroll
-            for (int tm = 0; tm < TM; ++tm) {
-                bf16x8 a[3][2];
-#pragma unroll
-                for (int t = 0; t < 3; ++t)
-#pragma unroll
-                    for (int h = 0; h < 2; ++h)
-                        a[t][h] = *(const bf16x8 *)(as + t * PLANE + (tm * 16 + li) * XLD + 16 * q + 8 * h);
-#pragma unroll
-                for (int tn = 0; tn < TN; ++tn) {
-                    floatx4 blk = floatx4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                    for (int t = 2; t >= 0; --t)
-#pragma unroll
-                        for (int h = 0; h < 2; ++h)
-                            blk = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[t][h], b[bu][tn][h], blk, 0, 0, 0);
-                    const float sc_u = live ? s[bu][tn] : 0.0f;
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) acc[tm][tn][r] = __builtin_fmaf(blk[r], sc_u, acc[tm][tn][r]);
-                }
-            }
+            x3_block<TM, TN>(As[u], li, q, b[bu], s[bu], live, acc);
             // block g+1's activations -> the other stage, then refill with block g+3
             amax = fmaxf(amax, xstore_a<TM>(As[v], tid, areg[v]));
             __builtin_amdgcn_sched_barrier(0);
@@ -714,28 +729,7 @@ __global__ __launch_bounds__(256, 2) void gemm_x3_kernel(const GemmArgs G, float
                     SRQ_CONVERT(v, v);
                     SRQ_LOAD_B(min(g + 3, glast), v);
                 }
-                const __bf16 *as = As[u];
-#pragma unroll
-                for (int tm = 0; tm < TM; ++tm) {
-                    bf16x8 a[3][2];
-#pragma unroll
-                    for (int t = 0; t < 3; ++t)
-#pragma unroll
-                        for (int h = 0; h < 2; ++h)
-                            a[t][h] = *(const bf16x8 *)(as + t * PLANE + (tm * 16 + li) * XLD + 16 * q + 8 * h);
-#pragma unroll
-                    for (int tn = 0; tn < TN; ++tn) {
-                        floatx4 blk = floatx4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                        for (int t = 2; t >= 0; --t)
-#pragma unroll
-                            for (int h = 0; h < 2; ++h)
-                                blk = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[t][h], b[bu][tn][h], blk, 0, 0, 0);
-                        const float sc_u = live ? s[bu][tn] : 0.0f;
-#pragma unroll
-                        for (int r = 0; r < 4; ++r) acc[tm][tn][r] = __builtin_fmaf(blk[r], sc_u, acc[tm][tn][r]);
-                    }
-                }
+                x3_block<TM, TN>(As[u], li, q, b[bu], s[bu], live, acc);
                 // block g+1's activations -> the other stage, then refill with block g+3
                 amax = fmaxf(amax, xstore_a<TM>(As[v], tid, areg[v]));
                 SRQ_LOAD_A(min(g + 3, glast), v);
