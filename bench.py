@@ -347,9 +347,9 @@ def bench_q4mixed_prefill(srq, args):
     # One untimed chunk on a throwaway cache first, as every other mode warms
     # up: the first 256-row step loads its kernels' code and sizes the step
     # workspace (about 7 ms, once per process).
-    warm = pool.cache((chunk + 31) // 32)
-    model.step([warm], [prompt[:chunk]])
-    warm.close()
+    warm_cache = pool.cache((chunk + 31) // 32)
+    model.step([warm_cache], [prompt[:chunk]])
+    warm_cache.close()
     ex.synchronize()
     chunk_ms = []
     for lo in range(0, prompt_n, chunk):
@@ -360,10 +360,12 @@ def bench_q4mixed_prefill(srq, args):
         chunk_ms.append(hip.elapsed_ms(a, b))
     first = int(model.argmax_last()[0])
     dec = srq.Decoder(model, cache, first, gen - 1, eager=args.eager)
+    warm = min(4, (gen - 1) // 4)  # untimed decode steps: the decode kernels' first launches
+    dec.run(warm)
     ex.synchronize()
     a, b = hip.create(), hip.create()
     hip.record(a, stream)
-    dec.run(gen - 1)
+    dec.run(gen - 1 - warm)
     hip.record(b, stream)
     dec_ms = hip.elapsed_ms(a, b)
     dec.close()
@@ -381,7 +383,7 @@ def bench_q4mixed_prefill(srq, args):
         "layer_gemm_tflops_per_chunk": round(2.0 * chunk * params / 1e12, 3),
         "achieved_tflops_mean": round(flops_chunk * len(chunk_ms) / prefill_s / 1e12, 2),
         "fp32_mfma_peak_tflops": 157.3,
-        "decode_tokens_per_s": round((gen - 1) / (dec_ms / 1e3), 1),
+        "decode_tokens_per_s": round((gen - 1 - warm) / (dec_ms / 1e3), 1),
         "decode_weight_bytes_per_token": synthetic.decode_weight_bytes(cfg, "q4-mixed"),
         "resident_weight_bytes": model.resident_bytes()}), flush=True)
     return 0
@@ -496,9 +498,12 @@ def bench_longctx_decode(srq, args):
     model = synthetic.build(ex, cfg, "q8", args.seed)
     hip = HipEvents()
     stream = C.c_void_p(ex.stream)
-    pool = model.pool((prompt_n + gen) // 32 + 2)
+    pool = model.pool((prompt_n + gen) // 32 + 2 + chunk // 32)
     cache = pool.cache((prompt_n + gen + 31) // 32)
     prompt = synthetic.random_prompt(prompt_n, cfg.vocab, args.seed)
+    warm_cache = pool.cache((chunk + 31) // 32)  # one untimed chunk, as in the prefill bench
+    model.step([warm_cache], [prompt[:chunk]])
+    warm_cache.close()
     ex.synchronize()
     a, b = hip.create(), hip.create()
     hip.record(a, stream)
@@ -508,9 +513,11 @@ def bench_longctx_decode(srq, args):
     prefill_ms = hip.elapsed_ms(a, b)
     first = int(model.argmax_last()[0])
     dec = srq.Decoder(model, cache, first, gen - 1, eager=args.eager)
+    warm = min(4, (gen - 1) // 4)  # untimed decode steps: the decode kernels' first launches
+    dec.run(warm)
     ex.synchronize()
     hip.record(a, stream)
-    dec.run(gen - 1)
+    dec.run(gen - 1 - warm)
     hip.record(b, stream)
     dec_ms = hip.elapsed_ms(a, b)
     dec.close()
@@ -518,7 +525,7 @@ def bench_longctx_decode(srq, args):
     wbytes = synthetic.decode_weight_bytes(cfg, "q8")
     mid = prompt_n + gen // 2
     kv_bytes = 2 * mid * kd * 4 * cfg.layers
-    tok_s = (gen - 1) / (dec_ms / 1e3)
+    tok_s = (gen - 1 - warm) / (dec_ms / 1e3)
     print(json.dumps({
         "metric": "Mistral-7B-shape Q8 long-context greedy decode tokens/s (paged KV)",
         "value": round(tok_s, 1), "unit": "tokens/s", "n_gpus": 1, "higher_is_better": True,
@@ -527,7 +534,7 @@ def bench_longctx_decode(srq, args):
                                "tokens" % (prompt_n, gen), "seed": args.seed,
                    "decode_launch": "eager" if args.eager else "hip-graph"},
         "prefill_tokens_per_s": round(prompt_n / (prefill_ms / 1e3), 1),
-        "decode_ms_per_token": round(dec_ms / (gen - 1), 4),
+        "decode_ms_per_token": round(dec_ms / (gen - 1 - warm), 4),
         "weight_bytes_per_token": wbytes, "kv_bytes_per_token_mid": kv_bytes,
         "achieved_gb_per_s": round((wbytes + kv_bytes) * tok_s / 1e9, 1),
         "frac_of_hbm_peak": round((wbytes + kv_bytes) * tok_s / 8e12, 4)}), flush=True)

@@ -75,15 +75,20 @@ struct DevBuf {
     size_t n = 0;
 };
 
+// Grows b to at least `bytes`.  A buffer that has to grow again takes half
+// as much again as it held, so steps whose shapes creep up (the attention
+// scratch gains a split every 64 positions) reallocate -- a stream
+// synchronisation, a free and an allocation -- a logarithmic number of times.
 int ensure(DevBuf &b, size_t bytes, hipStream_t s) {
     if (bytes <= b.n) return SRQ_OK;
+    size_t want = std::max(bytes, (size_t)256);
     if (b.p) {
+        want = std::max(want, b.n + b.n / 2);
         SRQ_HIP(hipStreamSynchronize(s));
         SRQ_HIP(hipFree(b.p));
         b.p = nullptr;
         b.n = 0;
     }
-    size_t want = std::max(bytes, (size_t)256);
     if (hipMalloc(&b.p, want) != hipSuccess) {
         b.p = nullptr;
         return fail(SRQ_ENOMEM, "device allocation of %zu bytes failed", want);
