@@ -1444,14 +1444,19 @@ extern "C" int srq_sample(srq_exec *e, const float *logits, int32_t rows, const 
     uint64_t *d_rng = (uint64_t *)d;
     int32_t *d_ids = d + 2 * rows, *d_blk = d + 3 * rows, *d_hl = d + 4 * rows, *d_rows = d + 5 * rows;
     int32_t *d_hist = d + 6 * rows;
-    SRQ_HIP(hipMemcpyAsync(d_rng, rng_state, (size_t)rows * 8, hipMemcpyHostToDevice, e->stream));
-    if (blocked) SRQ_HIP(hipMemcpyAsync(d_blk, blocked, (size_t)rows * 4, hipMemcpyHostToDevice, e->stream));
-    if (row_ids) SRQ_HIP(hipMemcpyAsync(d_rows, row_ids, (size_t)rows * 4, hipMemcpyHostToDevice, e->stream));
-    if (history) {
-        SRQ_HIP(hipMemcpyAsync(d_hl, history_len, (size_t)rows * 4, hipMemcpyHostToDevice, e->stream));
-        if (hist_words)
-            SRQ_HIP(hipMemcpyAsync(d_hist, history, hist_words * 4, hipMemcpyHostToDevice, e->stream));
+    // The per-row words go through the pinned staging buffer (free: every
+    // call ends synchronised) as one copy each way; copies from pageable
+    // memory would each stage and wait on their own.
+    SRQ_CHECK(ensure_host_meta(e, (size_t)rows * 6));
+    int32_t *h = e->h_meta;
+    std::memcpy(h, rng_state, (size_t)rows * 8);
+    for (int32_t r = 0; r < rows; ++r) {
+        h[3 * rows + r] = blocked ? blocked[r] : 0;
+        h[4 * rows + r] = history ? history_len[r] : 0;
+        h[5 * rows + r] = row_ids ? row_ids[r] : 0;
     }
+    SRQ_HIP(hipMemcpyAsync(d, h, (size_t)rows * 6 * 4, hipMemcpyHostToDevice, e->stream));
+    if (hist_words) SRQ_HIP(hipMemcpyAsync(d_hist, history, hist_words * 4, hipMemcpyHostToDevice, e->stream));
     SampleArgs a{};
     a.logits = logits;
     a.row_ids = row_ids ? d_rows : nullptr;
@@ -1469,10 +1474,12 @@ extern "C" int srq_sample(srq_exec *e, const float *logits, int32_t rows, const 
     a.ids = d_ids;
     a.err = e->d_err;
     SRQ_CHECK(launch_sample(e->stream, a, ws.SMPS.p));
-    SRQ_HIP(hipMemcpyAsync(ids, d_ids, (size_t)rows * 4, hipMemcpyDeviceToHost, e->stream));
-    SRQ_HIP(hipMemcpyAsync(rng_state, d_rng, (size_t)rows * 8, hipMemcpyDeviceToHost, e->stream));
+    // [rng: 2*rows][ids: rows] back in one copy
+    SRQ_HIP(hipMemcpyAsync(h, d, (size_t)rows * 3 * 4, hipMemcpyDeviceToHost, e->stream));
     SRQ_HIP(hipMemcpyAsync(e->h_err, e->d_err, sizeof(int32_t) * 4, hipMemcpyDeviceToHost, e->stream));
     SRQ_HIP(hipStreamSynchronize(e->stream));
+    std::memcpy(rng_state, h, (size_t)rows * 8);
+    std::memcpy(ids, h + 2 * rows, (size_t)rows * 4);
     const int32_t err = e->h_err[0];
     if (err) {
         SRQ_HIP(hipMemsetAsync(e->d_err, 0, sizeof(int32_t) * 4, e->stream));
