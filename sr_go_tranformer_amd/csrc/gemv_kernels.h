@@ -924,6 +924,18 @@ __global__ __launch_bounds__(kStreamThreads) void gemv_stream_kernel(const GemvA
             lu += nwaves;
             lch = 0;
             set_rows(lu);
+        } else {
+            // Past the wave's last step the cursor parks on the activations
+            // (at least as many bytes as a row's chunks and its scales), which
+            // every workgroup has just staged, so they sit in L2: re-reading
+            // each wave's own last steps cost 11% extra HBM traffic at four
+            // rows per step (Q4, 28672x4096).
+            lch = 0;
+#pragma unroll
+            for (int i = 0; i < R; ++i) {
+                lw[i] = (const uint8_t *)A.x;
+                if constexpr (FMT != SRQ_F32) ls[i] = A.x;
+            }
         }
     };
     // The first staging pass (and the q/k/v launch's RoPE rows and KV
