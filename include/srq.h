@@ -265,7 +265,10 @@ int srq_cache_read(srq_exec *e, const srq_cache *c, int32_t layer, int32_t pos0,
  * runs stops it within about 8 to 12 layers;
  * nonzero => SRQ_ECANCELED once the layers already queued have drained, no
  * positions committed.  Without a flag the step is queued whole.
- * logits_host (nullable) receives a host copy. */
+ * logits_host (nullable) receives a host copy.  With neither logits_host
+ * nor a cancel flag the call returns once the step is queued (positions
+ * committed): the executor's later calls run after it on its stream, and a
+ * device fault surfaces at the next call that waits for the stream. */
 int srq_step(srq_exec *e, srq_model *m, int32_t sessions, srq_cache *const *caches, const int32_t *chunk_lens,
              const int32_t *tokens, const uint8_t *want, float **logits, float *logits_host,
              const volatile int32_t *cancel);

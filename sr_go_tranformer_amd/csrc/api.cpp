@@ -168,6 +168,8 @@ struct srq_exec {
     Workspace ws;
     int32_t *h_meta = nullptr;  // pinned metadata staging
     size_t h_meta_n = 0;
+    int32_t *h_smp = nullptr;   // pinned staging of srq_sample's per-row words
+    size_t h_smp_n = 0;
     hipEvent_t layer_done[2] = {};  // in-flight cancellation: progress events of the last layer groups
 };
 
@@ -445,6 +447,7 @@ static void exec_unref(srq_exec *e) {
     if (e->d_err) (void)hipFree(e->d_err);
     if (e->h_err) (void)hipHostFree(e->h_err);
     if (e->h_meta) (void)hipHostFree(e->h_meta);
+    if (e->h_smp) (void)hipHostFree(e->h_smp);
     for (hipEvent_t ev : e->layer_done)
         if (ev) (void)hipEventDestroy(ev);
     if (e->stream) (void)hipStreamDestroy(e->stream);
@@ -1400,7 +1403,10 @@ extern "C" int srq_step(srq_exec *e, srq_model *m, int32_t sessions, srq_cache *
         rc = launch_gather_rows(e->stream, as<float>(ws.LOGC), m->c.vocab, dm.expand, sessions, as<float>(ws.LOG));
         out = as<float>(ws.LOG);
     }
-    hipError_t he = hipStreamSynchronize(e->stream);
+    // With neither a host copy nor a cancel flag the step returns queued:
+    // the executor's later calls run after it on the same stream.
+    const bool queued = !logits_host && !cancel;
+    hipError_t he = queued ? hipSuccess : hipStreamSynchronize(e->stream);
     if (rc != SRQ_OK) return rc;
     if (he != hipSuccess) return fail(SRQ_EDEVICE, "step failed: %s", hipGetErrorString(he));
     if (cancel && *cancel) return fail(SRQ_ECANCELED, "context canceled");
@@ -1444,11 +1450,19 @@ extern "C" int srq_sample(srq_exec *e, const float *logits, int32_t rows, const 
     uint64_t *d_rng = (uint64_t *)d;
     int32_t *d_ids = d + 2 * rows, *d_blk = d + 3 * rows, *d_hl = d + 4 * rows, *d_rows = d + 5 * rows;
     int32_t *d_hist = d + 6 * rows;
-    // The per-row words go through the pinned staging buffer (free: every
-    // call ends synchronised) as one copy each way; copies from pageable
-    // memory would each stage and wait on their own.
-    SRQ_CHECK(ensure_host_meta(e, (size_t)rows * 6));
-    int32_t *h = e->h_meta;
+    // The per-row words go through a pinned staging buffer of their own (a
+    // queued step may still be copying the metadata buffer; the previous
+    // sampling call ended synchronised) as one copy each way: copies from
+    // pageable memory would each stage and wait on their own.
+    if ((size_t)rows * 6 > e->h_smp_n) {
+        if (e->h_smp) (void)hipHostFree(e->h_smp);
+        e->h_smp = nullptr;
+        e->h_smp_n = 0;
+        const size_t want = std::max<size_t>((size_t)rows * 6, 1536);
+        if (hipHostMalloc((void **)&e->h_smp, want * 4) != hipSuccess) return fail(SRQ_ENOMEM, "pinned allocation failed");
+        e->h_smp_n = want;
+    }
+    int32_t *h = e->h_smp;
     std::memcpy(h, rng_state, (size_t)rows * 8);
     for (int32_t r = 0; r < rows; ++r) {
         h[3 * rows + r] = blocked ? blocked[r] : 0;
