@@ -126,6 +126,35 @@ def test_step_validation_never_mutates(ex):
     assert np.all(np.isfinite(out)) and c.pos == 4
 
 
+def test_queued_step_equals_waited_step(ex):
+    """srq_step with neither a host copy nor a cancel flag returns once the
+    step is queued: positions are committed at once, and the device logits
+    and K/V rows that later calls read are, bit for bit, those of the same
+    steps made with a host copy (which wait for the device)."""
+    fx = hf_fixtures.load("llama_f32")
+    m = gpu_models.load_fixture(ex, fx, "q8")
+    pool = m.pool(8)
+    a, b = pool.cache(3), pool.cache(3)
+    ids = [int(t) for t in fx.ids[:10]]
+    for lo in range(0, len(ids), 4):
+        want = m.step([a], [ids[lo:lo + 4]])
+    for lo in range(0, len(ids), 4):
+        dev = m.step([b], [ids[lo:lo + 4]], host=False)
+        assert b.pos == min(lo + 4, len(ids))
+    got = np.empty_like(want)
+    srq.check(srq.lib().srq_copy_d2h(ex.h, got.ctypes.data_as(C.c_void_p), dev, got.nbytes))
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    for layer in range(fx.layers):
+        ka, va = a.read(layer, 0, len(ids))
+        kb, vb = b.read(layer, 0, len(ids))
+        assert np.array_equal(ka.view(np.uint32), kb.view(np.uint32)), layer
+        assert np.array_equal(va.view(np.uint32), vb.view(np.uint32)), layer
+    a.close()
+    b.close()
+    pool.close()
+    m.close()
+
+
 def test_greedy_generate_and_decoder(ex):
     fx = hf_fixtures.load("mistral_f32")
     for fmt in ("q8", "q4-mixed"):
