@@ -313,11 +313,15 @@ RowMeta make_meta(srq_exec *e, srq_model *m, int layer, int32_t pt_stride, const
 // Rows above which srq_linear takes the MFMA GEMM: up to here a row's bits
 // do not depend on the batch (the GEMV computes rows independently).
 constexpr int32_t kLinearGemmRows = 16;
-// Rows above which a step's layers take the MFMA GEMM (with separate norm,
-// RoPE and SwiGLU kernels): from 9 rows the GEMV would stream every weight
-// twice (8 rows per pass).  Continuous-batching steps of 9-16 rows run
-// 14% faster this way (Llama-3.2-3B shape, 32 sessions).
-constexpr int32_t kStepGemmRows = 8;
+// Rows above which a step's layers and its head take the MFMA GEMM (with
+// separate norm, RoPE and SwiGLU kernels).  At 5-8 rows the GEMM and its
+// reduction beat the GEMV (Llama-3.2-3B shape: gate/up 33 against 21 us,
+// q/k/v 23 against 15 us, down 31 us as two 4-row GEMV passes -- 8 rows of
+// 8192 activations exceed LDS -- against 19 us; the 128256-id head 164
+// against about 128 us); at 3-4 rows they are even or the GEMV wins.
+// Continuous batching (32 sessions): 1311 -> 1349 tokens/s against a
+// boundary at 8 rows.
+constexpr int32_t kStepGemmRows = 4;
 
 // Device scratch the GEMM of y = x . W^T needs for n rows (split-K partial
 // sums and wide-row flags); 0 on the GEMV path.
@@ -1296,9 +1300,9 @@ int enqueue_layers(srq_exec *e, Workspace &ws, srq_model *m, srq_pool *pool, int
 int enqueue_head(srq_exec *e, Workspace &ws, srq_model *m, const float *rows, int32_t heads) {
     const srq_weight &head = m->has_output ? m->output : m->embed;
     float *N = as<float>(ws.N), *LOGC = as<float>(ws.LOGC);
-    if (heads > 16 && gemm_ok(head.fmt, m->c.dim)) {
+    if (heads > kStepGemmRows && gemm_ok(head.fmt, m->c.dim)) {
         SRQ_CHECK(launch_rmsnorm(e->stream, rows, m->final_norm, N, heads, m->c.dim, m->c.norm_eps));
-        return run_linear(e, ws, head, N, heads, LOGC, m->c.vocab, nullptr, 0.0, nullptr);
+        return run_linear(e, ws, head, N, heads, LOGC, m->c.vocab, nullptr, 0.0, nullptr, kStepGemmRows);
     }
     return run_linear(e, ws, head, rows, heads, LOGC, m->c.vocab, m->final_norm, m->c.norm_eps, nullptr);
 }

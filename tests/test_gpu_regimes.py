@@ -1,6 +1,6 @@
 """Rows computed by different paths, on the GPU through the C ABI.
 
-A step's linear layers run as GEMVs up to 8 rows and as MFMA GEMMs above;
+A step's linear layers run as GEMVs up to 4 rows and as MFMA GEMMs above;
 attention runs split kernels or, for prefill-sized steps, the flash
 kernel.  Each path is deterministic and batch invariant on its own, but a
 row's bits can differ between paths.  The reference holds its engine's
@@ -75,21 +75,22 @@ def generate_direct(ex, m, pool, prompt, params, seed, count, chunk=16):
 
 @pytest.mark.parametrize("fmt", ["q8", "q4", "q4-mixed"])
 def test_engine_streams_equal_direct_generation(ex, fmt):
-    """TestLowBitEngineSharedModelAndStreams (q8_cli_test.go:123-188): eight
-    identical requests at the default sampled settings, run through the
+    """TestLowBitEngineSharedModelAndStreams (q8_cli_test.go:123-188): four
+    identical requests at the default sampled settings (the reference
+    runs eight; four keep the last steps on the GEMV), run through the
     engine's ticks (TickPlanner: budget 64, prefill chunk 16, mixed chunk
     1) with three companion requests, each produce the completion of direct
-    generation.  The companions leave once the eight hold 6 outputs, so the
-    eight decode in steps of 11 rows (MFMA GEMM) and then of 8 (GEMV),
-    while the direct run decodes in steps of one row (GEMV)."""
+    generation.  The companions leave once the four hold 6 outputs, so the
+    four decode in steps of 7 rows (MFMA GEMM) and then of 4 (GEMV), while
+    the direct run decodes in steps of one row (GEMV)."""
     cfg = small_config()
     m, _ = gpu_models.synthetic(ex, cfg, fmt, seed=23)
     prompt = syn.random_prompt(40, cfg.vocab, 5)
     out_n = 12
     pool = m.pool(96)
     want = generate_direct(ex, m, pool, prompt, DEFAULT, 1, out_n)
-    prompts = [prompt] * 8 + [syn.random_prompt(n, cfg.vocab, 100 + n) for n in (6, 9, 12)]
-    seeds = [1] * 8 + [7, 8, 9]
+    prompts = [prompt] * 4 + [syn.random_prompt(n, cfg.vocab, 100 + n) for n in (6, 9, 12)]
+    seeds = [1] * 4 + [7, 8, 9]
     tp = TickPlanner(prompts, 10 * out_n, 64, 16, 1)
     caches = [pool.cache((len(p) + 10 * out_n + 31) // 32) for p in prompts]
     states = np.array(seeds, np.uint64)
@@ -107,17 +108,17 @@ def test_engine_streams_equal_direct_generation(ex, fmt):
             for j, k in enumerate(sel):
                 states[sessions[k]] = st[j]
                 sampled[sessions[k]] = int(ids[j])
-        if any(i < 8 and tp.cursor[i] >= len(prompts[i]) for i in sessions):
+        if any(i < 4 and tp.cursor[i] >= len(prompts[i]) for i in sessions):
             rows_seen.add(sum(len(c) for c in chunks))
         tp.commit(sampled)
-        # companions leave once the eight hold 6 outputs; each of the eight
+        # companions leave once the four hold 6 outputs; each of the four
         # after out_n
         for i in list(tp.live):
-            if (i >= 8 and len(tp.outputs[0]) >= 6) or (i < 8 and len(tp.outputs[i]) >= out_n):
+            if (i >= 4 and len(tp.outputs[0]) >= 6) or (i < 4 and len(tp.outputs[i]) >= out_n):
                 tp.live.remove(i)
-    print("decode steps of the eight: row counts", sorted(rows_seen), flush=True)
-    assert any(r >= 9 for r in rows_seen) and any(r <= 8 for r in rows_seen), rows_seen
-    for i in range(8):
+    print("decode steps of the four: row counts", sorted(rows_seen), flush=True)
+    assert any(r >= 5 for r in rows_seen) and any(r <= 4 for r in rows_seen), rows_seen
+    for i in range(4):
         assert tp.outputs[i] == want, (fmt, i, tp.outputs[i], want)
     for c in caches:
         c.close()
@@ -129,7 +130,7 @@ def test_engine_streams_equal_direct_generation(ex, fmt):
 def test_chunked_prefill_kv_rows_and_completions_match_tokenwise(ex, fmt):
     """TestPromptPrefillExactCompletionAndKV (prompt_prefill_test.go:91-120):
     for every prompt length there, prefill in chunks of 16 rows and of the
-    whole prompt (MFMA GEMM from 9 rows; the flash kernel for prefill-sized
+    whole prompt (MFMA GEMM from 5 rows; the flash kernel for prefill-sized
     steps) against one row per step (GEMV): the last logits and every
     committed K/V row of both layers within 1e-4, and completions sampled at
     temperature 0 and 0.7 (seed 19, 8 tokens) identical."""
@@ -186,7 +187,7 @@ def decode_row_logits(ex, m, cfg, prompt, companions, seed):
 @pytest.mark.timeout(900)
 def test_draw_flip_probability_between_paths(ex):
     """How often a sampled draw changes when a decode row's logits come from
-    a step of 9 rows (MFMA GEMM) instead of 8 (GEMV): per context, 65536
+    a step of 5 rows (MFMA GEMM) instead of 4 (GEMV): per context, 65536
     draws from the same RNG states over both logit rows.  The rate depends
     on how many candidates lie within the logits' difference of each other:
       - the small model at the default settings (top-k 40): none;
@@ -207,7 +208,7 @@ def test_draw_flip_probability_between_paths(ex):
         flips, dmax, total = [0] * len(settings), 0.0, 0
         for ctx in range(contexts):
             prompt = syn.random_prompt(24 + 37 * ctx, cfg.vocab, 200 + ctx)
-            rows = [decode_row_logits(ex, m, cfg, prompt, comp, 300 + ctx) for comp in (7, 8)]
+            rows = [decode_row_logits(ex, m, cfg, prompt, comp, 300 + ctx) for comp in (3, 4)]
             dmax = max(dmax, float(np.abs(rows[0].astype(np.float64) - rows[1]).max()))
             buf = srq.DeviceBuffer.from_numpy(ex, np.stack(rows).astype(np.float32))
             seeds = np.arange(1, draws + 1, dtype=np.uint64) * np.uint64(0x9E3779B97F4A7C15)
@@ -222,7 +223,7 @@ def test_draw_flip_probability_between_paths(ex):
             total += draws
         for s_i, (params, bound) in enumerate(settings):
             rate = flips[s_i] / total
-            print("%s, T %g top-k %d top-p %g: %d of %d draws differ between the 8- and 9-row paths (%.2e per "
+            print("%s, T %g top-k %d top-p %g: %d of %d draws differ between the 4- and 5-row paths (%.2e per "
                   "draw); max |logit diff| %.3g (%.1f s)" % (name, params.temperature, params.top_k, params.top_p,
                                                             flips[s_i], total, rate, dmax, time.time() - t0),
                   flush=True)
