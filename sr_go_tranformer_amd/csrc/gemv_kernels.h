@@ -898,18 +898,22 @@ __global__ __launch_bounds__(kStreamThreads) void gemv_stream_kernel(const GemvA
     float eb[P][RG];  // EPI_RESID: the units' residual values, carried with each step
     // group_start: constant once the ring is unrolled (slot % G == 0).
     auto load_next = [&](uint4(&w)[R], float(&sc)[R], float(&e)[RG], const bool group_start) {
-        const bool ok = (int64_t)lch * CW + (int64_t)lane * E < cols;
-        const int boff = ok ? lch * 1024 + lane * 16 : 0;
+        // Wave-major rows are whole 1 KiB chunks, so every lane is inside.
+        // The offsets are 32-bit unsigned so that each load adds them to its
+        // row's scalar base in the instruction (no 64-bit vector adds).
+        const bool ok = WMAJOR || (int64_t)lch * CW + (int64_t)lane * E < cols;
+        const uint32_t boff = ok ? (uint32_t)(lch * 1024 + lane * 16) : 0u;
         // G > 1: lane l loads scale l of the group (l mod G*SPC: Q8 with
         // G = 2 needs 32), in bounds since rows are whole groups of chunks.
         // The group is the one holding lch: a cursor parked on a wave's last
         // step (any chunk of the row) still reads inside its row.
-        const int soff = G == 1 ? (ok ? lch * SPC + lane_sc : 0) : (lch & ~(G - 1)) * SPC + (lane & (G * SPC - 1));
+        const uint32_t soff = G == 1 ? (ok ? (uint32_t)(lch * SPC + lane_sc) : 0u)
+                                     : (uint32_t)((lch & ~(G - 1)) * SPC + (lane & (G * SPC - 1)));
 #pragma unroll
         for (int i = 0; i < R; ++i) {
             w[i] = ld_stream16(lw[i] + boff);
             if constexpr (FMT != SRQ_F32) {
-                if (group_start) sc[i] = ls[i][soff];
+                if (group_start) sc[i] = *(const float *)((const uint8_t *)ls[i] + soff * 4u);
             } else {
                 sc[i] = 1.0f;
             }
