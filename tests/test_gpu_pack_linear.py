@@ -258,16 +258,18 @@ def test_linear_gemm_unrolled_slices(ex, shape):
     assert np.array_equal(got48[:20].view(np.uint32), got20.view(np.uint32))
 
 
+@pytest.mark.parametrize("fmt", [srq.Q8, srq.Q4])
 @pytest.mark.parametrize("shape", [(200, 1024, 40), (200, 1024, 20), (1000, 256, 40), (1000, 256, 20)])
-def test_linear_gemm_wide_rows(ex, shape):
+def test_linear_gemm_wide_rows(ex, shape, fmt):
     """Wide rows found by split-K slices (K = 1024) and by whole-K tiles
-    (K = 256), with 32- and 64-row tiles."""
+    (K = 256), with 32- and 64-row tiles (Q4 64-row tiles: 8 waves)."""
     rows, cols, n = shape
+    print("gemm wide rows", fmt, shape, flush=True)
     x, dense = oracle.linear_fixture(n, cols, rows)
     x = x.copy()
     x[3, 5] = FMAX / np.float32(4)
     x[n - 3, 100] = np.float32(-1e37)
-    w, ow = _weights(ex, dense * np.float32(0.001), srq.Q8)
+    w, ow = _weights(ex, dense * np.float32(0.001), fmt)
     got = srq.linear(ex, w, x)
     near(got, oracle.linear_closed_f64(ow, x), 2e-5)
 
