@@ -514,9 +514,9 @@ __device__ __forceinline__ void x3_finish(const GemmArgs &G, float *__restrict__
         float *P = partial + (int64_t)blockIdx.z * G.n * G.rows;
         if (blockIdx.x == 0 && tid < BM && m0 + tid < G.n) wflags[(int64_t)blockIdx.z * G.n + m0 + tid] = row_wide[tid];
         const int64_t nw = (int64_t)blockIdx.x * XBN;  // the workgroup's first feature
-        if (m0 + BM <= G.n && nw + XBN <= G.rows) {
-            // Every output of the workgroup is in bounds (a uniform test):
-            // 32-bit offsets from its corner, no per-store checks.
+        if (m0 + BM <= G.n && nw + XBN <= G.rows && G.rows * BM < (int64_t(1) << 30)) {
+            // Every output of the workgroup is in bounds (a uniform test) and
+            // its byte offsets from the corner fit 32 bits: no per-store checks.
             float *Pt = P + m0 * G.rows + nw;
             const uint32_t ld = (uint32_t)G.rows, c0 = (uint32_t)(n0 - nw) + (uint32_t)li;
 #pragma unroll
