@@ -1173,10 +1173,16 @@ struct GemmPlan {
 // (rows, cols) and never on n, so a row's bits are the same whatever other
 // rows share the call (batch invariance, q8_test.go:88-92).  It is the count
 // that fills the chip for one 32-row tile of outputs: with fewer feature
-// tiles than CUs, slices of at least 256 inputs bring the grid to one
-// workgroup per CU (each slice's partial sums cost as much traffic as a
-// share of the weights, which outweighs a second resident workgroup).
-// Larger n adds row tiles to the same slices.
+// tiles than CUs, slices of at least 256 inputs bring the grid to at most
+// one workgroup per CU (each slice's partial sums cost as much traffic as a
+// share of the weights, which outweighs a second resident workgroup).  The
+// count rounds down: rounding up left a few CUs with two workgroups that
+// finished last (3072 x 8192 at 32 rows: 24 x 11 = 264 workgroups, the
+// slowest waves 4.6 us behind the median), and rounding down also halves
+// some large-n partial traffic (Llama-3.2-3B continuous batching 1363 ->
+// 1402 tokens/s, Mistral-7B q4-mixed prefill 15.30k -> 16.43k, 8.2k-token
+// Q8 prefill 12.45k -> 12.74k).  Larger n adds row tiles to the same
+// slices.
 GemmPlan plan_gemm(int fmt, int32_t n, int64_t rows, int64_t cols) {
     GemmPlan p;
     p.x3 = (fmt == SRQ_Q8 || fmt == SRQ_Q4) && cols % kBlock == 0;
@@ -1198,7 +1204,7 @@ GemmPlan plan_gemm(int fmt, int32_t n, int64_t rows, int64_t cols) {
     const int ksteps = (int)(cols / bk), min_steps = kMinSliceInputs / bk;
     int slices = 1;
     if (tiles < kCUs)
-        slices = (int)std::max<int64_t>(1, std::min<int64_t>((kCUs + tiles - 1) / tiles, ksteps / min_steps));
+        slices = (int)std::max<int64_t>(1, std::min<int64_t>(kCUs / tiles, ksteps / min_steps));
     p.kper = (ksteps + slices - 1) / slices;
     p.slices = (ksteps + p.kper - 1) / p.kper;
     return p;
@@ -1206,7 +1212,7 @@ GemmPlan plan_gemm(int fmt, int32_t n, int64_t rows, int64_t cols) {
 
 template <int TM, int TN, int KU = 4>
 void launch_unrolled(hipStream_t s, dim3 grid, const GemmArgs &a, float *partial, int32_t *wflags, int kper) {
-    if constexpr (KU <= 12) {
+    if constexpr (KU <= 16) {
         if (kper == KU)
             gemm_x3_kernel<SRQ_Q8, TM, TN, KU><<<grid, 256, 0, s>>>(a, partial, wflags, kper);
         else
@@ -1221,7 +1227,7 @@ constexpr int kPairDist = 4;
 
 template <int TM, int TN, int NW, int KU = 4>
 void launch_pairs(hipStream_t s, dim3 grid, const GemmArgs &a, float *partial, int32_t *wflags, int kper) {
-    if constexpr (KU <= 12) {
+    if constexpr (KU <= 16) {
         if (kper == KU)
             gemm_x3p_kernel<TM, TN, NW, KU, kPairDist<TN>><<<grid, 64 * NW, 0, s>>>(a, partial, wflags, kper);
         else
@@ -1239,10 +1245,10 @@ void launch_tiles(hipStream_t s, const GemmArgs &a, const GemmPlan &p, float *pa
         if (p.x3) {
             const int xbn = 64 * p.tn;
             dim3 grid((unsigned)((a.rows + xbn - 1) / xbn), (unsigned)((a.n + BMT - 1) / BMT), (unsigned)p.slices);
-            // Q8 slices of 4..12 blocks run unrolled; at 16 and 32 rows with
+            // Q8 slices of 4..16 blocks run unrolled; at 16 and 32 rows with
             // whole 128-byte row segments (cols % 128 == 0), pair-streamed
             if constexpr (BMT <= 32) {
-                if (FMT == SRQ_Q8 && p.kper >= 4 && p.kper <= 12 && a.cols % (2 * kBlock) == 0 &&
+                if (FMT == SRQ_Q8 && p.kper >= 4 && p.kper <= 16 && a.cols % (2 * kBlock) == 0 &&
                     (uint64_t)a.rows * (uint64_t)a.cols <= UINT32_MAX) {
                     // the plan's feature tile (64 * tn); 256 features over 8 waves
                     // (gate/up 16384x3072 at 17-32 rows: 24.5 -> 22.6 us; 128
@@ -1262,7 +1268,7 @@ void launch_tiles(hipStream_t s, const GemmArgs &a, const GemmPlan &p, float *pa
             }
             if constexpr (BMT == 16) {
                 if (p.tn == 1) {
-                    if (FMT == SRQ_Q8 && p.kper >= 4 && p.kper <= 12)
+                    if (FMT == SRQ_Q8 && p.kper >= 4 && p.kper <= 16)
                         launch_unrolled<1, 1>(s, grid, a, partial, wflags, p.kper);
                     else
                         gemm_x3_kernel<FMT, 1, 1, 0><<<grid, 256, 0, s>>>(a, partial, wflags, p.kper);
@@ -1283,7 +1289,7 @@ void launch_tiles(hipStream_t s, const GemmArgs &a, const GemmPlan &p, float *pa
                     return;
                 }
             }
-            if (FMT == SRQ_Q8 && p.kper >= 4 && p.kper <= 12) {
+            if (FMT == SRQ_Q8 && p.kper >= 4 && p.kper <= 16) {
                 if (p.tn == 2)
                     launch_unrolled<BMT / 16, 2>(s, grid, a, partial, wflags, p.kper);
                 else

@@ -234,16 +234,16 @@ def test_linear_gemm_mfma(ex, fmt, n, shape):
     assert np.array_equal(got2.view(np.uint32), got[perm].view(np.uint32))
 
 
-# (rows, cols) -> K slices of 5..12 64-input blocks (the Q8 kernel's
-# unrolled instantiations), last slices ragged, 1000 rows a partial tile;
-# 16384 rows take 256-feature tiles.
+# (rows, cols) -> K slices of 5..16 64-input blocks (the Q8 kernel's
+# unrolled instantiations: 5120 x 5120 takes 14, 7168 x 4096 16), last
+# slices ragged, 1000 rows a partial tile; 16384 rows take 256-feature tiles.
 UNROLLED_SHAPES = [(3072, 3072), (4096, 3072), (5120, 3072), (4096, 4096), (8192, 2304), (5120, 4096),
-                   (6144, 4096), (3072, 8192), (16384, 3072), (1000, 704)]
+                   (6144, 4096), (3072, 8192), (16384, 3072), (1000, 704), (5120, 5120), (7168, 4096)]
 
 
 @pytest.mark.parametrize("shape", UNROLLED_SHAPES)
 def test_linear_gemm_unrolled_slices(ex, shape):
-    """Q8 GEMM whose K slices hold 5..12 blocks, at 20 rows (32-row tiles)
+    """Q8 GEMM whose K slices hold 5..16 blocks, at 20 rows (32-row tiles)
     and 48 rows (64-row tiles): against the oracle, and the 20 rows keep
     their bits in the 48-row launch."""
     print("gemm unrolled", shape, flush=True)
