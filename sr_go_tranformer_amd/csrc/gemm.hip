@@ -1220,6 +1220,17 @@ void launch_unrolled(hipStream_t s, dim3 grid, const GemmArgs &a, float *partial
     }
 }
 
+// The same for any format and NW waves (the Q4 64-row tiles).
+template <int FMT, int TM, int TN, int NW, int KU = 4>
+void launch_unrolled_nw(hipStream_t s, dim3 grid, const GemmArgs &a, float *partial, int32_t *wflags, int kper) {
+    if constexpr (KU <= 16) {
+        if (kper == KU)
+            gemm_x3_kernel<FMT, TM, TN, KU, NW><<<grid, 64 * NW, 0, s>>>(a, partial, wflags, kper);
+        else
+            launch_unrolled_nw<FMT, TM, TN, NW, KU + 1>(s, grid, a, partial, wflags, kper);
+    }
+}
+
 // Pair-streamed Q8 tiles (gemm_x3p_kernel): blocks between a block's
 // weight loads and its MFMAs.
 template <int TN>
@@ -1283,9 +1294,14 @@ void launch_tiles(hipStream_t s, const GemmArgs &a, const GemmPlan &p, float *pa
                 // Each tile's arithmetic is unchanged.  Q8, which converts its
                 // codes just before their MFMAs, ran slower so (8.2k-token
                 // prefill 12.15k -> 11.99k, continuous batching 1355 -> 1336).
+                // Slices of 4..16 blocks run unrolled (prefill 16.49k ->
+                // 16.60k tokens/s).
                 if (p.tn == 4) {
                     const dim3 g8((unsigned)((a.rows + 511) / 512), grid.y, grid.z);
-                    gemm_x3_kernel<FMT, 4, 4, 0, 8><<<g8, 512, 0, s>>>(a, partial, wflags, p.kper);
+                    if (p.kper >= 4 && p.kper <= 16)
+                        launch_unrolled_nw<FMT, 4, 4, 8>(s, g8, a, partial, wflags, p.kper);
+                    else
+                        gemm_x3_kernel<FMT, 4, 4, 0, 8><<<g8, 512, 0, s>>>(a, partial, wflags, p.kper);
                     return;
                 }
             }
