@@ -138,6 +138,20 @@ def test_step_rows_independent_of_batch_q4_tiles(ex):
         assert same_bits(out[n], out[9]), n
 
 
+def test_step_rows_independent_of_batch_wide_slices(ex):
+    """Llama-3.2-3B widths (dim 3072, 8 KV heads of 128, FFN 8192), one
+    layer: the down projection's K slices hold 13 blocks, so steps of 5, 8
+    and 16 rows (16-row pair-streamed tiles), 17 and 32 (32-row pair-streamed
+    tiles) and 33 and 64 (64-row unrolled tiles) run three kernels over the
+    same slices; a decode row keeps the 5-row step's bits (and the oracle's
+    logits within 1e-4)."""
+    print("wide-slice step invariance", flush=True)
+    cfg = srq.make_config(512, 3072, 1, 24, 8, 8192, 200, 10000.0, 1e-5, True)
+    out = _step_alone_and_in_batches(ex, cfg, 61, 40, (5, 8, 16, 17, 32, 33, 64))
+    for n in (8, 16, 17, 32, 33, 64):
+        assert same_bits(out[n], out[5]), n
+
+
 def test_step_rows_independent_of_batch_row_groups(ex):
     """Steps of 3 and 4 rows stream the 4100-unit gate/up GEMV two units
     per step and the 8200-id head four rows per step (row groups, the last
